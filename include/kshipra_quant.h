@@ -1,0 +1,107 @@
+/*
+ * kshipra_quant.h -- C ABI of the MI355X (gfx950) weight-only quantized
+ * linear path: symmetric per-output-channel INT8 and symmetric per-group INT4
+ * quantize/pack, dequantize, and the fused dequant-matmul.
+ *
+ * Each entry point replaces one function of Kshipra's engine/quantization.py
+ * (cited per declaration).  Conventions shared by every entry point:
+ *
+ *  - All pointers are device pointers (HIP global memory) owned by the caller;
+ *    the library never allocates or frees them.  Matrices are row-major with
+ *    an explicit leading dimension in elements.
+ *  - fp16 values (scales) travel as their IEEE binary16 bit patterns (uint16).
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream).  Work is
+ *    enqueued on it; no entry point synchronises the host.
+ *  - Return value: KQ_OK, or an error code with a message retrievable through
+ *    kq_last_error() (per calling thread).  Argument errors are detected on
+ *    the host before any launch.  No C++ exception crosses this boundary.
+ */
+#ifndef KSHIPRA_QUANT_H
+#define KSHIPRA_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* kq_stream_t; /* hipStream_t */
+
+enum kq_status {
+  KQ_OK = 0,
+  KQ_ERR_ARG = 1,         /* bad shape / dtype / group size / alignment: maps to QuantizationError */
+  KQ_ERR_HIP = 2,         /* a HIP runtime error: maps to RuntimeError */
+  KQ_ERR_WORKSPACE = 3    /* workspace missing or too small */
+};
+
+enum kq_dtype { KQ_F32 = 0, KQ_F16 = 1, KQ_BF16 = 2 };
+
+/* ABI version (major * 100 + minor); bump on any signature change. */
+int kq_version(void);
+
+/* Message for the last non-OK status returned on this thread. */
+const char* kq_last_error(void);
+
+/* Replaces the finiteness pass of _validate_weight, engine/quantization.py:187.
+ * Sets *nonfinite_flag (device int32) to 1 if any w[r, c] (r < n, c < k) is
+ * NaN or +-inf, else to 0. */
+int kq_check_finite(const void* w, int w_dtype, int64_t n, int64_t k, int64_t ldw,
+                    int32_t* nonfinite_flag, kq_stream_t stream);
+
+/* Replaces quantize_int8_per_channel, engine/quantization.py:196-223.
+ * w: [n, k] (ldw) of w_dtype.  payload: int8 [n, k] contiguous.  scales: fp16
+ * bits [n].  Bit-exact with the reference: s = fp16(max(|w_r| / 127, 1e-8)),
+ * q = clamp(rint(w / float(s)), -127, 127), NaN -> 0.  *nonfinite_flag is set
+ * as by kq_check_finite (the caller discards the outputs when it is 1). */
+int kq_quantize_int8(const void* w, int w_dtype, int64_t n, int64_t k, int64_t ldw,
+                     int8_t* payload, uint16_t* scales, int32_t* nonfinite_flag,
+                     kq_stream_t stream);
+
+/* Replaces quantize_int4_per_group, engine/quantization.py:238-318.
+ * group_size: positive and even.  k_padded = ceil(k / group_size) * group_size.
+ * payload: uint8 [n, k_padded / 2] (low nibble = even column).  scales: fp16
+ * bits [n, k_padded / group_size].  Columns k..k_padded-1 are zero padding. */
+int kq_quantize_int4(const void* w, int w_dtype, int64_t n, int64_t k, int64_t ldw,
+                     int64_t group_size, uint8_t* payload, uint16_t* scales,
+                     int32_t* nonfinite_flag, kq_stream_t stream);
+
+/* Replaces _dequantize_int8_per_channel (engine/quantization.py:226-230) and
+ * the cast of QuantizedWeight.dequantize (:161-172).  out: [n, k] contiguous
+ * of out_dtype; the exact fp32 product q * s rounded to out_dtype (RNE). */
+int kq_dequantize_int8(const int8_t* payload, const uint16_t* scales, int64_t n, int64_t k,
+                       void* out, int out_dtype, kq_stream_t stream);
+
+/* Replaces _dequantize_int4_per_group (engine/quantization.py:321-344) and the
+ * cast of :172.  out: [n, k] contiguous (the padding is sliced off). */
+int kq_dequantize_int4(const uint8_t* payload, const uint16_t* scales, int64_t n, int64_t k,
+                       int64_t group_size, int64_t k_padded, void* out, int out_dtype,
+                       kq_stream_t stream);
+
+/* Workspace (device bytes) that kq_linear_int8 / kq_linear_int4 need for
+ * these sizes; 0 when none.  scheme: 8 or 4. */
+size_t kq_linear_workspace_bytes(int scheme, int64_t m, int64_t n, int64_t k, int64_t group_size);
+
+/* Replaces QuantizedLinear.forward for scheme "int8" (engine/quantization.py:
+ * 394-396 over the payload of :196-223): y[m, n] = sum_k x[m, k] * q[n, k] *
+ * s[n] + bias[n], fp32 in and out, fp32 accumulation.  x: [m, k] (ldx),
+ * y: [m, n] (ldy), bias: [n] or NULL.  workspace: at least
+ * kq_linear_workspace_bytes(8, ...) bytes (may be NULL when that is 0). */
+int kq_linear_int8(const float* x, int64_t m, int64_t ldx, const int8_t* payload,
+                   const uint16_t* scales, const float* bias, float* y, int64_t ldy,
+                   int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                   kq_stream_t stream);
+
+/* Replaces QuantizedLinear.forward for scheme "int4" (engine/quantization.py:
+ * 394-396 over the payload of :238-318): y[m, n] = sum_k x[m, k] * q[n, k] *
+ * s[n, k / group_size] + bias[n] over the first k columns. */
+int kq_linear_int4(const float* x, int64_t m, int64_t ldx, const uint8_t* payload,
+                   const uint16_t* scales, int64_t group_size, int64_t k_padded,
+                   const float* bias, float* y, int64_t ldy, int64_t n, int64_t k,
+                   void* workspace, size_t workspace_bytes, kq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KSHIPRA_QUANT_H */

@@ -1,0 +1,185 @@
+"""Caller side of the quantized-linear path: the projection swap and a greedy
+decoder that runs every projection through ``QuantizedLinear`` on the GPU.
+
+* ``quantize_all_linears(hf_model, scheme)`` -- Kshipra ``engine/model.py:80-91``:
+  swaps q/k/v/o and gate/up/down of every decoder layer of a HuggingFace
+  Llama / Qwen2 model for ``QuantizedLinear`` (always ``group_size=128``);
+  embeddings and lm_head stay unquantized.  Move the model to the GPU first
+  (``engine/model.py:67``): the quantized payload is created on the weight's
+  device.
+* ``DecoderLM`` -- a decoder-only LM over a plain weight dict with the op order
+  of ``KshipraModel.forward`` (``engine/model.py:93-151``) and the greedy loop
+  of ``generate`` (``:153-205``): one prefill forward over the prompt (M = prompt
+  length), then M = 1 decode steps, first-index argmax.  The seven projections
+  of each layer are ``QuantizedLinear`` modules (the hot path); RMSNorm, RoPE,
+  attention over a contiguous KV cache and the fp32 lm_head are plain torch
+  ops on the same device and stream.
+
+Weight dict keys (HF naming): ``embed_tokens.weight``, ``norm.weight``,
+``lm_head.weight``, ``layers.{i}.{q,k,v,o,gate,up,down}_proj.weight``,
+``layers.{i}.{q,k,v}_proj.bias`` (Qwen2), ``layers.{i}.input_layernorm.weight``,
+``layers.{i}.post_attention_layernorm.weight``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .quantization import QuantizedLinear
+
+PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def quantize_all_linears(model: nn.Module, scheme: str, group_size: int = 128) -> nn.Module:
+    """engine/model.py:80-91: swap the 7 projections of every layer in place."""
+    for layer in model.model.layers:
+        attn, mlp = layer.self_attn, layer.mlp
+        attn.q_proj = QuantizedLinear(attn.q_proj, scheme=scheme, group_size=group_size)
+        attn.k_proj = QuantizedLinear(attn.k_proj, scheme=scheme, group_size=group_size)
+        attn.v_proj = QuantizedLinear(attn.v_proj, scheme=scheme, group_size=group_size)
+        attn.o_proj = QuantizedLinear(attn.o_proj, scheme=scheme, group_size=group_size)
+        mlp.gate_proj = QuantizedLinear(mlp.gate_proj, scheme=scheme, group_size=group_size)
+        mlp.up_proj = QuantizedLinear(mlp.up_proj, scheme=scheme, group_size=group_size)
+        mlp.down_proj = QuantizedLinear(mlp.down_proj, scheme=scheme, group_size=group_size)
+    return model
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    vocab_size: int
+    hidden_size: int
+    intermediate_size: int
+    num_layers: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    rope_theta: float = 1000000.0
+    rms_norm_eps: float = 1e-6
+    qkv_bias: bool = True
+
+    def proj_shape(self, name: str) -> Tuple[int, int]:
+        h, i, d = self.hidden_size, self.intermediate_size, self.head_dim
+        return {
+            "q_proj": (self.num_heads * d, h),
+            "k_proj": (self.num_kv_heads * d, h),
+            "v_proj": (self.num_kv_heads * d, h),
+            "o_proj": (h, self.num_heads * d),
+            "gate_proj": (i, h),
+            "up_proj": (i, h),
+            "down_proj": (h, i),
+        }[name]
+
+
+def _rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    var = x.pow(2).mean(-1, keepdim=True)
+    return w * (x * torch.rsqrt(var + eps))
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat([-x2, x1], dim=-1)
+
+
+class DecoderLM:
+    """Greedy decoder whose projections are ``QuantizedLinear`` (INT8 / INT4)."""
+
+    def __init__(self, cfg: DecoderConfig, weights: Dict[str, torch.Tensor], scheme: str,
+                 device: torch.device, group_size: int = 128, max_seq: int = 256) -> None:
+        self.cfg = cfg
+        self.device = device
+        dev = lambda t: torch.as_tensor(t).to(device=device, dtype=torch.float32)
+        self.embed = dev(weights["embed_tokens.weight"])
+        self.norm = dev(weights["norm.weight"])
+        self.lm_head = dev(weights["lm_head.weight"])
+        self.layers: List[Dict[str, object]] = []
+        for li in range(cfg.num_layers):
+            layer: Dict[str, object] = {
+                "in_norm": dev(weights[f"layers.{li}.input_layernorm.weight"]),
+                "post_norm": dev(weights[f"layers.{li}.post_attention_layernorm.weight"]),
+            }
+            for p in PROJ:
+                out_f, in_f = cfg.proj_shape(p)
+                bias_key = f"layers.{li}.{p}.bias"
+                lin = nn.Linear(in_f, out_f, bias=bias_key in weights, device=device)
+                with torch.no_grad():
+                    lin.weight.copy_(dev(weights[f"layers.{li}.{p}.weight"]))
+                    if bias_key in weights:
+                        lin.bias.copy_(dev(weights[bias_key]))
+                layer[p] = QuantizedLinear(lin, scheme=scheme, group_size=group_size)
+                del lin
+            self.layers.append(layer)
+        exps = torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim
+        self.inv_freq = (1.0 / (cfg.rope_theta ** exps)).to(device)
+        self.max_seq = max_seq
+        self.reset()
+
+    def reset(self) -> None:
+        c = self.cfg
+        shape = (c.num_layers, c.num_kv_heads, self.max_seq, c.head_dim)
+        self.k_cache = torch.zeros(shape, dtype=torch.float32, device=self.device)
+        self.v_cache = torch.zeros(shape, dtype=torch.float32, device=self.device)
+        self.pos = 0
+
+    @torch.inference_mode()
+    def forward(self, ids: List[int]) -> torch.Tensor:
+        """Logits [L, vocab] for the next L tokens (engine/model.py:93-151)."""
+        c = self.cfg
+        L = len(ids)
+        if self.pos + L > self.max_seq:
+            raise RuntimeError("KV cache capacity exceeded")
+        pos = torch.arange(self.pos, self.pos + L, device=self.device, dtype=torch.float32)
+        freqs = pos[:, None] * self.inv_freq[None, :]
+        emb = torch.cat([freqs, freqs], dim=-1)
+        cos, sin = emb.cos(), emb.sin()
+        h = self.embed[torch.as_tensor(ids, device=self.device)]
+        g = c.num_heads // c.num_kv_heads
+        scale = 1.0 / math.sqrt(c.head_dim)
+        S = self.pos + L
+        qpos = torch.arange(self.pos, S, device=self.device)
+        kpos = torch.arange(S, device=self.device)
+        mask = kpos[None, :] > qpos[:, None]
+        for li, layer in enumerate(self.layers):
+            res = h
+            x = _rms_norm(h, layer["in_norm"], c.rms_norm_eps)
+            q = layer["q_proj"](x).view(L, c.num_heads, c.head_dim).transpose(0, 1)
+            k = layer["k_proj"](x).view(L, c.num_kv_heads, c.head_dim).transpose(0, 1)
+            v = layer["v_proj"](x).view(L, c.num_kv_heads, c.head_dim).transpose(0, 1)
+            q = q * cos[None] + _rotate_half(q) * sin[None]
+            k = k * cos[None] + _rotate_half(k) * sin[None]
+            self.k_cache[li, :, self.pos:S] = k
+            self.v_cache[li, :, self.pos:S] = v
+            kc = self.k_cache[li, :, :S].repeat_interleave(g, dim=0).contiguous()
+            vc = self.v_cache[li, :, :S].repeat_interleave(g, dim=0).contiguous()
+            s = torch.matmul(q.contiguous(), kc.transpose(1, 2).contiguous()) * scale
+            s = s.masked_fill(mask[None], float("-inf"))
+            p = torch.softmax(s, dim=-1)
+            a = torch.matmul(p, vc).transpose(0, 1).reshape(L, c.num_heads * c.head_dim)
+            h = res + layer["o_proj"](a.contiguous())
+            res = h
+            x = _rms_norm(h, layer["post_norm"], c.rms_norm_eps)
+            act = F.silu(layer["gate_proj"](x)) * layer["up_proj"](x)
+            h = res + layer["down_proj"](act)
+        self.pos = S
+        h = _rms_norm(h, self.norm, c.rms_norm_eps)
+        return F.linear(h, self.lm_head)
+
+    @torch.inference_mode()
+    def generate(self, prompt: List[int], max_new_tokens: int,
+                 eos_token_id: Optional[int] = None) -> Tuple[List[int], List[torch.Tensor]]:
+        """engine/model.py:153-205 greedy loop; returns (tokens, per-step logits)."""
+        self.reset()
+        logits = self.forward(prompt)[-1]
+        toks, all_logits = [int(torch.argmax(logits).item())], [logits]
+        for _ in range(1, max_new_tokens):
+            if eos_token_id is not None and toks[-1] == eos_token_id:
+                break
+            logits = self.forward([toks[-1]])[-1]
+            toks.append(int(torch.argmax(logits).item()))
+            all_logits.append(logits)
+        return toks, all_logits

@@ -1,0 +1,360 @@
+"""Weight-only INT8 / INT4 quantization on MI355X -- drop-in for Kshipra's
+``engine/quantization.py``.
+
+Same public names, fields, scheme strings, dtypes, shapes, validation and
+error types as the reference module:
+
+* ``QuantizationError``            (engine/quantization.py:69-70)
+* ``QuantizedWeight``              (:78-172)  payload / scales / scheme /
+  original_shape / group_size / in_features_padded; ``storage_bytes()``;
+  ``dequantize(dtype=torch.float16)``
+* ``_validate_weight``             (:180-188)
+* ``quantize_int8_per_channel``    (:196-223)
+* ``_dequantize_int8_per_channel`` (:226-230)
+* ``quantize_int4_per_group``      (:238-318)
+* ``_dequantize_int4_per_group``   (:321-344)
+* ``QuantizedLinear``              (:352-403)
+
+Layouts are the reference's: INT8 payload ``int8 [out, in]`` with fp16 scales
+``[out]``; INT4 payload ``uint8 [out, in_padded // 2]`` (low nibble = even
+column, two's-complement nibbles) with fp16 scales ``[out, in_padded // G]``.
+
+What differs is where the work runs.  Every compute entry point launches a
+hand-written gfx950 HIP kernel from ``libkshipra_quant.so`` on the tensor's
+device and torch's current stream:
+
+* quantize / pack: bit-exact with the reference (true fp32 division, fp16
+  round-to-nearest-even scale, round-half-to-even, NaN -> 0, +-inf -> clamp);
+* ``QuantizedLinear.forward``: the fused dequant-matmul -- the packed payload
+  is streamed once from HBM and never materialised; fp32 accumulation;
+* ``dequantize``: exact ``q * s`` rounded to the requested dtype.
+
+Tensors must live on a ROCm GPU.  A CPU tensor raises ``RuntimeError``: there
+is no CPU fallback.  As in the reference, ``QuantizedWeight`` is a plain
+attribute of ``QuantizedLinear`` (not a buffer), so move the float module to
+the GPU *before* quantizing (engine/model.py:67,77-78 does exactly that).
+
+Activations of dtype float16 / bfloat16 are computed in fp32 and the output is
+rounded to the input dtype once (the reference instead rounds the weight to
+that dtype first; the fp32 path is the more accurate of the two).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from ._errors import QuantizationError
+
+__all__ = [
+    "QuantizationError",
+    "QuantizedWeight",
+    "quantize_int8_per_channel",
+    "quantize_int4_per_group",
+    "QuantizedLinear",
+]
+
+
+# ---------------------------------------------------------------------- #
+# Container (engine/quantization.py:78-172)
+# ---------------------------------------------------------------------- #
+
+
+@dataclass
+class QuantizedWeight:
+    """A quantized weight tensor plus the metadata needed to dequantize it.
+
+    payload:            ``int8 [out, in]`` (INT8) or ``uint8 [out, in_padded // 2]`` (INT4)
+    scales:             fp16 ``[out]`` (INT8) or ``[out, in_padded // group_size]`` (INT4)
+    scheme:             ``"int8_per_channel"`` or ``"int4_per_group"``
+    original_shape:     ``(out_features, in_features)``
+    group_size:         ``G`` for INT4, ``None`` for INT8
+    in_features_padded: ``ceil(in / G) * G`` for INT4, ``None`` for INT8
+    """
+
+    payload: torch.Tensor
+    scales: torch.Tensor
+    scheme: str
+    original_shape: Tuple[int, int]
+    group_size: Optional[int] = None
+    in_features_padded: Optional[int] = None
+
+    def __post_init__(self) -> None:
+        # Same checks and messages as engine/quantization.py:108-152.
+        if self.scheme not in ("int8_per_channel", "int4_per_group"):
+            raise QuantizationError(f"unknown scheme {self.scheme!r}")
+        out_features, _ = self.original_shape
+        if self.scales.shape[0] != out_features:
+            raise QuantizationError(
+                f"scales.shape[0] = {self.scales.shape[0]} does not match "
+                f"out_features = {out_features}")
+        if self.scheme == "int8_per_channel":
+            if self.payload.dtype != torch.int8:
+                raise QuantizationError(f"INT8 payload must be int8, got {self.payload.dtype}")
+            if self.scales.dim() != 1:
+                raise QuantizationError(
+                    f"INT8 scales must be 1-D [out_features], got {tuple(self.scales.shape)}")
+            if tuple(self.payload.shape) != tuple(self.original_shape):
+                raise QuantizationError(
+                    f"INT8 payload shape {tuple(self.payload.shape)} != "
+                    f"original_shape {self.original_shape}")
+        else:
+            if self.payload.dtype != torch.uint8:
+                raise QuantizationError(f"INT4 payload must be uint8, got {self.payload.dtype}")
+            if self.group_size is None or self.in_features_padded is None:
+                raise QuantizationError("INT4 requires group_size and in_features_padded")
+            expected_groups = self.in_features_padded // self.group_size
+            if tuple(self.scales.shape) != (out_features, expected_groups):
+                raise QuantizationError(
+                    f"INT4 scales shape {tuple(self.scales.shape)} != "
+                    f"({out_features}, {expected_groups})")
+            expected_payload_cols = self.in_features_padded // 2
+            if tuple(self.payload.shape) != (out_features, expected_payload_cols):
+                raise QuantizationError(
+                    f"INT4 payload shape {tuple(self.payload.shape)} != "
+                    f"({out_features}, {expected_payload_cols})")
+
+    def storage_bytes(self) -> int:
+        """Bytes occupied by payload + scales (engine/quantization.py:154-159)."""
+        return (self.payload.numel() * self.payload.element_size()
+                + self.scales.numel() * self.scales.element_size())
+
+    def dequantize(self, dtype: torch.dtype = torch.float16) -> torch.Tensor:
+        """Materialise ``original_shape`` in ``dtype`` (engine/quantization.py:161-172).
+
+        The fp32 product ``q * s`` is exact; it is rounded to ``dtype`` once.
+        """
+        if self.scheme == "int8_per_channel":
+            return _dequantize_int8_per_channel(self, dtype)
+        return _dequantize_int4_per_group(self, dtype)
+
+
+# ---------------------------------------------------------------------- #
+# Helpers
+# ---------------------------------------------------------------------- #
+
+
+def _validate_dims(w: torch.Tensor) -> None:
+    if w.dim() != 2:
+        raise QuantizationError(f"weight must be 2-D, got {w.dim()}-D")
+    if w.shape[0] == 0 or w.shape[1] == 0:
+        raise QuantizationError(f"weight must have non-zero dims, got {tuple(w.shape)}")
+
+
+def _weight_view(w: torch.Tensor) -> Tuple[torch.Tensor, int, int]:
+    """fp32/fp16/bf16 view with unit column stride, and its kernel dtype code /
+    leading dimension.  Other float dtypes are rounded to fp32 first, as
+    ``w.to(torch.float32)`` does at engine/quantization.py:205."""
+    w = w.detach()
+    if w.dtype not in _lib.DTYPE_CODE:
+        w = w.to(torch.float32)
+    if w.stride(1) != 1 or (w.shape[0] > 1 and w.stride(0) < w.shape[1]):
+        w = w.contiguous()
+    ld = w.stride(0) if w.shape[0] > 1 else w.shape[1]
+    return w, _lib.DTYPE_CODE[w.dtype], ld
+
+
+def _raise_if_nonfinite(flag: torch.Tensor) -> None:
+    if int(flag.item()) != 0:
+        raise QuantizationError("weight contains non-finite values")
+
+
+def _validate_weight(w: torch.Tensor) -> None:
+    """engine/quantization.py:180-188: 2-D, non-empty, all finite (GPU pass)."""
+    _validate_dims(w)
+    _lib.require_device(w, "weight")
+    lib = _lib.load()
+    wv, code, ld = _weight_view(w)
+    flag = torch.empty(1, dtype=torch.int32, device=w.device)
+    _lib.check(lib.kq_check_finite(wv.data_ptr(), code, wv.shape[0], wv.shape[1], ld,
+                                   flag.data_ptr(), _lib.stream_of(wv)))
+    _raise_if_nonfinite(flag)
+
+
+# ---------------------------------------------------------------------- #
+# INT8 per-channel (engine/quantization.py:196-230)
+# ---------------------------------------------------------------------- #
+
+
+def quantize_int8_per_channel(w: torch.Tensor) -> QuantizedWeight:
+    """Symmetric per-output-channel INT8 quantization, bit-exact with the reference.
+
+    ``s[r] = fp16(max(max|W[r, :]| / 127, 1e-8))``; ``q = clamp(rint(W / s), -127, 127)``.
+    One HIP kernel computes the row maxima, the scales and the payload; the
+    finiteness check of :187 is fused into it.
+    """
+    _validate_dims(w)
+    _lib.require_device(w, "weight")
+    lib = _lib.load()
+    wv, code, ld = _weight_view(w)
+    n, k = wv.shape
+    payload = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    scales = torch.empty((n,), dtype=torch.float16, device=w.device)
+    flag = torch.empty(1, dtype=torch.int32, device=w.device)
+    _lib.check(lib.kq_quantize_int8(wv.data_ptr(), code, n, k, ld, payload.data_ptr(),
+                                    scales.data_ptr(), flag.data_ptr(), _lib.stream_of(wv)))
+    _raise_if_nonfinite(flag)
+    return QuantizedWeight(payload=payload, scales=scales, scheme="int8_per_channel",
+                           original_shape=(int(n), int(k)))
+
+
+def _out_dtype(dtype: torch.dtype) -> torch.dtype:
+    return dtype if dtype in _lib.DTYPE_CODE else torch.float32
+
+
+def _dequantize_int8_per_channel(qw: QuantizedWeight,
+                                 dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """engine/quantization.py:226-230: ``q * s`` (exact in fp32), as ``dtype``."""
+    _lib.require_device(qw.payload, "payload")
+    lib = _lib.load()
+    n, k = qw.original_shape
+    od = _out_dtype(dtype)
+    out = torch.empty((n, k), dtype=od, device=qw.payload.device)
+    p, s = qw.payload.contiguous(), qw.scales.contiguous()
+    _lib.check(lib.kq_dequantize_int8(p.data_ptr(), s.data_ptr(), n, k, out.data_ptr(),
+                                      _lib.DTYPE_CODE[od], _lib.stream_of(p)))
+    return out if od == dtype else out.to(dtype)
+
+
+# ---------------------------------------------------------------------- #
+# INT4 per-group (engine/quantization.py:238-344)
+# ---------------------------------------------------------------------- #
+
+
+def quantize_int4_per_group(w: torch.Tensor, group_size: int = 128) -> QuantizedWeight:
+    """Symmetric per-group INT4 quantization with nibble packing, bit-exact.
+
+    ``G`` must be positive and even.  ``in_features`` is right-padded with
+    zeros to a multiple of ``G``; ``s[r, g] = fp16(max(max|group| / 7, 1e-8))``;
+    ``q = clamp(rint(W / s), -8, 7)``; ``byte[j] = (q[2j] & 0xF) | (q[2j+1] & 0xF) << 4``.
+    """
+    _validate_dims(w)
+    if group_size <= 0 or group_size % 2 != 0:
+        raise QuantizationError(f"group_size must be a positive even integer, got {group_size}")
+    _lib.require_device(w, "weight")
+    lib = _lib.load()
+    wv, code, ld = _weight_view(w)
+    n, k = wv.shape
+    num_groups = (k + group_size - 1) // group_size
+    kp = num_groups * group_size
+    payload = torch.empty((n, kp // 2), dtype=torch.uint8, device=w.device)
+    scales = torch.empty((n, num_groups), dtype=torch.float16, device=w.device)
+    flag = torch.empty(1, dtype=torch.int32, device=w.device)
+    _lib.check(lib.kq_quantize_int4(wv.data_ptr(), code, n, k, ld, group_size,
+                                    payload.data_ptr(), scales.data_ptr(), flag.data_ptr(),
+                                    _lib.stream_of(wv)))
+    _raise_if_nonfinite(flag)
+    return QuantizedWeight(payload=payload, scales=scales, scheme="int4_per_group",
+                           original_shape=(int(n), int(k)), group_size=int(group_size),
+                           in_features_padded=int(kp))
+
+
+def _dequantize_int4_per_group(qw: QuantizedWeight,
+                               dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """engine/quantization.py:321-344: unpack, sign-restore, scale, slice to ``in``."""
+    assert qw.group_size is not None and qw.in_features_padded is not None
+    _lib.require_device(qw.payload, "payload")
+    lib = _lib.load()
+    n, k = qw.original_shape
+    od = _out_dtype(dtype)
+    out = torch.empty((n, k), dtype=od, device=qw.payload.device)
+    p, s = qw.payload.contiguous(), qw.scales.contiguous()
+    _lib.check(lib.kq_dequantize_int4(p.data_ptr(), s.data_ptr(), n, k, qw.group_size,
+                                      qw.in_features_padded, out.data_ptr(),
+                                      _lib.DTYPE_CODE[od], _lib.stream_of(p)))
+    return out if od == dtype else out.to(dtype)
+
+
+# ---------------------------------------------------------------------- #
+# Fused dequant-matmul (engine/quantization.py:394-396)
+# ---------------------------------------------------------------------- #
+
+
+def quantized_linear(x: torch.Tensor, qw: QuantizedWeight,
+                     bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``F.linear(x, qw.dequantize(x.dtype), bias)`` without materialising the
+    weight: one fused HIP dequant-matmul over the packed payload."""
+    _lib.require_device(x, "input")
+    out_features, in_features = qw.original_shape
+    if x.shape[-1] != in_features:
+        raise RuntimeError(
+            f"mat1 and mat2 shapes cannot be multiplied "
+            f"({x.numel() // max(x.shape[-1], 1)}x{x.shape[-1]} and {in_features}x{out_features})")
+    if x.device != qw.payload.device:
+        raise RuntimeError(f"input on {x.device} but weight on {qw.payload.device}")
+    lib = _lib.load()
+    out_dtype = x.dtype
+    x2 = x.reshape(-1, in_features)
+    if x2.dtype != torch.float32:
+        x2 = x2.to(torch.float32)
+    if x2.stride(1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < in_features):
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    y = torch.empty((m, out_features), dtype=torch.float32, device=x.device)
+    if m > 0:
+        b = None
+        if bias is not None:
+            b = bias.detach()
+            if b.dtype != torch.float32 or not b.is_contiguous():
+                b = b.to(torch.float32).contiguous()
+        ldx = x2.stride(0) if m > 1 else in_features
+        stream = _lib.stream_of(x2)
+        if qw.scheme == "int8_per_channel":
+            nbytes = lib.kq_linear_workspace_bytes(8, m, out_features, in_features, 0)
+            ws = _lib.workspace(x.device, stream, nbytes)
+            _lib.check(lib.kq_linear_int8(
+                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), _lib.ptr(b),
+                y.data_ptr(), out_features, out_features, in_features, _lib.ptr(ws), nbytes, stream))
+        else:
+            g = qw.group_size
+            nbytes = lib.kq_linear_workspace_bytes(4, m, out_features, in_features, g)
+            ws = _lib.workspace(x.device, stream, nbytes)
+            _lib.check(lib.kq_linear_int4(
+                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), g,
+                qw.in_features_padded, _lib.ptr(b), y.data_ptr(), out_features, out_features,
+                in_features, _lib.ptr(ws), nbytes, stream))
+    y = y.reshape(*x.shape[:-1], out_features)
+    return y if out_dtype == torch.float32 else y.to(out_dtype)
+
+
+# ---------------------------------------------------------------------- #
+# Module wrapper (engine/quantization.py:352-403)
+# ---------------------------------------------------------------------- #
+
+
+class QuantizedLinear(nn.Module):
+    """A drop-in replacement for ``nn.Linear`` with quantized weights.
+
+    ``forward(x) = x @ (q * s)^T + bias`` computed by the fused HIP
+    dequant-matmul; the bias stays a registered buffer in its original dtype.
+    """
+
+    def __init__(self, linear: nn.Linear, scheme: str = "int8", group_size: int = 128) -> None:
+        super().__init__()
+        if not isinstance(linear, nn.Linear):
+            raise QuantizationError(f"expected nn.Linear, got {type(linear).__name__}")
+        if scheme not in ("int8", "int4"):
+            raise QuantizationError(f"scheme must be 'int8' or 'int4', got {scheme!r}")
+        self.in_features = linear.in_features
+        self.out_features = linear.out_features
+        self.scheme = scheme
+        w = linear.weight.detach()
+        if scheme == "int8":
+            self.weight = quantize_int8_per_channel(w)
+        else:
+            self.weight = quantize_int4_per_group(w, group_size)
+        if linear.bias is not None:
+            self.register_buffer("bias", linear.bias.detach().clone())
+        else:
+            self.bias = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return quantized_linear(x, self.weight, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"scheme={self.scheme}, storage_bytes={self.weight.storage_bytes()}")

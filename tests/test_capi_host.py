@@ -1,0 +1,171 @@
+"""CPU-only checks of the C-ABI library and the host-side logic.
+
+No GPU is touched: the library is loaded, every symbol the header declares is
+resolved, and only entry points whose argument validation fails on the host
+(before any HIP call) are invoked.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+import torch.nn as nn
+
+from kshipra_amd import _lib
+from kshipra_amd.quantization import (QuantizationError, QuantizedLinear, QuantizedWeight,
+                                      _validate_weight, quantize_int4_per_group,
+                                      quantize_int8_per_channel)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kshipra_quant.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(kq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    syms = header_symbols()
+    assert len(syms) >= 10
+    for name in syms:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert sorted(n for n, _, _ in _lib.SIGNATURES) == syms
+
+
+def test_version():
+    assert _lib.load().kq_version() == _lib.ABI_VERSION
+
+
+def test_workspace_query_is_host_only():
+    lib = _lib.load()
+    # M = 1 INT4 / INT8 on Llama-3-8B shapes: activations fit in LDS, no workspace
+    assert lib.kq_linear_workspace_bytes(4, 1, 14336, 4096, 128) == 0
+    assert lib.kq_linear_workspace_bytes(8, 1, 4096, 14336, 0) == 0
+    # M = 8, K = 4096: staged in the workspace, 4 bytes per activation
+    assert lib.kq_linear_workspace_bytes(8, 8, 4096, 4096, 0) == 4 * 8 * 4096
+    # GEMM path: M rounded up to the 64-row tile
+    assert lib.kq_linear_workspace_bytes(4, 512, 14336, 4096, 128) == 4 * 512 * 4096
+    assert lib.kq_linear_workspace_bytes(4, 100, 64, 256, 128) == 4 * 128 * 256
+    # generic path (G != 128) needs none
+    assert lib.kq_linear_workspace_bytes(4, 64, 512, 512, 32) == 0
+    assert lib.kq_linear_workspace_bytes(4, 0, 10, 10, 128) == 0
+
+
+@pytest.mark.parametrize("call", [
+    lambda L: L.kq_quantize_int4(None, 0, 4, 128, 128, 3, None, None, None, None),
+    lambda L: L.kq_quantize_int4(1, 0, 4, 128, 128, 0, 1, 1, 1, None),
+    lambda L: L.kq_quantize_int4(1, 0, 4, 128, 128, 127, 1, 1, 1, None),
+    lambda L: L.kq_quantize_int8(1, 7, 4, 128, 128, 1, 1, 1, None),
+    lambda L: L.kq_quantize_int8(1, 0, 0, 128, 128, 1, 1, 1, None),
+    lambda L: L.kq_quantize_int8(1, 0, 4, 128, 64, 1, 1, 1, None),
+    lambda L: L.kq_dequantize_int4(1, 1, 4, 100, 128, 256, 1, 0, None),
+    lambda L: L.kq_dequantize_int8(1, 1, 4, 100, 1, 9, None),
+    lambda L: L.kq_linear_int8(1, 1, 10, 1, 1, None, 1, 20, 20, 100, None, 0, None),
+    lambda L: L.kq_linear_int4(1, 1, 128, 1, 1, 128, 100, None, 1, 20, 20, 100, None, 0, None),
+    lambda L: L.kq_linear_int4(1, 1, 128, 1, 1, 3, 128, None, 1, 20, 20, 128, None, 0, None),
+])
+def test_argument_errors_are_reported_before_launch(call):
+    lib = _lib.load()
+    status = call(lib)
+    assert status == _lib.KQ_ERR_ARG
+    assert lib.kq_last_error() not in (None, b"")
+
+
+def test_missing_workspace_is_reported():
+    lib = _lib.load()
+    # M = 8, K = 4096 needs a workspace; pointers are never dereferenced
+    st = lib.kq_linear_int8(1, 8, 4096, 1, 1, None, 1, 4096, 4096, 4096, None, 0, None)
+    assert st == _lib.KQ_ERR_WORKSPACE
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.check(st)
+
+
+def test_status_mapping():
+    with pytest.raises(QuantizationError):
+        _lib.check(_lib.KQ_ERR_ARG)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.KQ_ERR_HIP)
+    _lib.check(_lib.KQ_OK)
+
+
+# ---------------------------------------------------------------------- #
+# Python API: host-side validation (Kshipra tests/test_quantization.py
+# :189-245 restated where it needs no GPU)
+# ---------------------------------------------------------------------- #
+
+
+def test_odd_and_zero_group_size_rejected():
+    w = torch.randn(4, 128)
+    for g in (127, 0, -2):
+        with pytest.raises(QuantizationError):
+            quantize_int4_per_group(w, group_size=g)
+
+
+def test_bad_rank_and_empty_rejected():
+    for w in (torch.randn(8), torch.randn(2, 3, 4), torch.empty(0, 4), torch.empty(4, 0)):
+        with pytest.raises(QuantizationError):
+            quantize_int8_per_channel(w)
+        with pytest.raises(QuantizationError):
+            _validate_weight(w)
+
+
+def test_bad_scheme_and_module_type_rejected():
+    with pytest.raises(QuantizationError):
+        QuantizedLinear(nn.Linear(8, 8), scheme="int3")
+    with pytest.raises(QuantizationError):
+        QuantizedLinear(nn.Conv1d(8, 8, 1), scheme="int8")
+
+
+def test_cpu_tensors_fail_loudly():
+    """There is no CPU fallback: compute on a CPU tensor raises."""
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        quantize_int8_per_channel(torch.randn(4, 8))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        quantize_int4_per_group(torch.randn(4, 8))
+
+
+def test_quantized_weight_validation():
+    """engine/quantization.py:108-152 checks, with host tensors."""
+    ok8 = QuantizedWeight(torch.zeros(3, 5, dtype=torch.int8), torch.zeros(3, dtype=torch.float16),
+                          "int8_per_channel", (3, 5))
+    assert ok8.storage_bytes() == 15 + 6
+    ok4 = QuantizedWeight(torch.zeros(3, 64, dtype=torch.uint8), torch.zeros(3, 1, dtype=torch.float16),
+                          "int4_per_group", (3, 100), 128, 128)
+    assert ok4.storage_bytes() == 3 * 64 + 3 * 2
+    bad = [
+        dict(payload=torch.zeros(3, 5, dtype=torch.int8), scales=torch.zeros(3, dtype=torch.float16),
+             scheme="int2", original_shape=(3, 5)),
+        dict(payload=torch.zeros(3, 5, dtype=torch.int8), scales=torch.zeros(4, dtype=torch.float16),
+             scheme="int8_per_channel", original_shape=(3, 5)),
+        dict(payload=torch.zeros(3, 5, dtype=torch.uint8), scales=torch.zeros(3, dtype=torch.float16),
+             scheme="int8_per_channel", original_shape=(3, 5)),
+        dict(payload=torch.zeros(3, 5, dtype=torch.int8), scales=torch.zeros(3, 1, dtype=torch.float16),
+             scheme="int8_per_channel", original_shape=(3, 5)),
+        dict(payload=torch.zeros(3, 4, dtype=torch.int8), scales=torch.zeros(3, dtype=torch.float16),
+             scheme="int8_per_channel", original_shape=(3, 5)),
+        dict(payload=torch.zeros(3, 64, dtype=torch.int8), scales=torch.zeros(3, 1, dtype=torch.float16),
+             scheme="int4_per_group", original_shape=(3, 100), group_size=128, in_features_padded=128),
+        dict(payload=torch.zeros(3, 64, dtype=torch.uint8), scales=torch.zeros(3, 1, dtype=torch.float16),
+             scheme="int4_per_group", original_shape=(3, 100)),
+        dict(payload=torch.zeros(3, 64, dtype=torch.uint8), scales=torch.zeros(3, 2, dtype=torch.float16),
+             scheme="int4_per_group", original_shape=(3, 100), group_size=128, in_features_padded=128),
+        dict(payload=torch.zeros(3, 63, dtype=torch.uint8), scales=torch.zeros(3, 1, dtype=torch.float16),
+             scheme="int4_per_group", original_shape=(3, 100), group_size=128, in_features_padded=128),
+    ]
+    for kw in bad:
+        with pytest.raises(QuantizationError):
+            QuantizedWeight(**kw)
+
+
+def test_header_cites_reference_for_every_compute_entry_point():
+    text = open(HEADER).read()
+    for name in ("kq_quantize_int8", "kq_quantize_int4", "kq_dequantize_int8", "kq_dequantize_int4",
+                 "kq_linear_int8", "kq_linear_int4", "kq_check_finite"):
+        block = text[:text.index(name + "(")].rsplit("/*", 1)[-1]
+        assert "engine/quantization.py" in block, name
