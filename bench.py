@@ -1,0 +1,343 @@
+"""Benchmark of the weight-only quantized linear path on one MI355X.
+
+Headline workload: one Llama-3-8B decode step at M = 1 through all 32 layers x
+7 projections (q, k, v, o, gate, up, down) with INT4 G=128 weights, fp32
+activations -- every projection a distinct weight (3.6 GB INT4 / 7.0 GB INT8
+resident in HBM, far beyond the 256 MB MALL, so no repeat read is a cache hit).
+The 224 fused dequant-GEMV launches of a step are captured once in a HIP graph
+and replayed; ``value`` is algorithmic bytes (payload + scales + x + y) per
+step over the measured step time.
+
+Also reported (same JSON line):
+  * INT8 per-channel M = 1 sweep (same shapes);
+  * per-projection GB/s (events around graphs of 32 same-shape launches);
+  * skinny M = 8 / 32 / 64 sweeps (continuous-batching decode);
+  * INT4 prefill-chunk GEMM TFLOP/s (X [512 x 4096] through gate/up
+    [14336 x 4096], then [512 x 14336] through down);
+  * ``roofline``: the dominant kernel (gate/up projection dequant-GEMV) vs the
+    8 TB/s HBM peak;
+  * ``cpu_baseline``: the oracle's restatement of the reference forward
+    (materialise w_hat = q * s in fp32, then one fp32 BLAS GEMV) timed on this
+    host's cores over one layer (7 projections).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--eager] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from kshipra_amd import _lib  # noqa: E402
+from kshipra_amd.quantization import quantize_int4_per_group, quantize_int8_per_channel  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+LAYERS = 32
+SHAPES = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096),
+          ("o_proj", 4096, 4096), ("gate_proj", 14336, 4096), ("up_proj", 14336, 4096),
+          ("down_proj", 4096, 14336)]
+
+
+def algorithmic_bytes(m, n, k, scheme):
+    """payload + scales + x (fp32) + y (fp32), each counted once."""
+    w = n * k + 2 * n if scheme == "int8" else n * k // 2 + 2 * n * (k // 128)
+    return w + 4 * m * k + 4 * m * n
+
+
+class Proj:
+    """One quantized projection with direct C-ABI launches (no Python per call
+    beyond the ctypes call, so it can be captured into a graph)."""
+
+    def __init__(self, qw, n, k, scheme):
+        self.qw, self.n, self.k, self.scheme = qw, n, k, scheme
+        self.lib = _lib.load()
+
+    def launch(self, x, y, ws, ws_bytes, stream):
+        m = x.shape[0]
+        if self.scheme == "int8":
+            st = self.lib.kq_linear_int8(x.data_ptr(), m, self.k, self.qw.payload.data_ptr(),
+                                         self.qw.scales.data_ptr(), None, y.data_ptr(), self.n,
+                                         self.n, self.k, ws, ws_bytes, stream)
+        else:
+            st = self.lib.kq_linear_int4(x.data_ptr(), m, self.k, self.qw.payload.data_ptr(),
+                                         self.qw.scales.data_ptr(), 128, self.k, None,
+                                         y.data_ptr(), self.n, self.n, self.k, ws, ws_bytes, stream)
+        _lib.check(st)
+
+
+def build_layers(scheme, dev, seed, nlayers=LAYERS):
+    """``nlayers`` layers x 7 projections, N(0, 0.02) weights drawn on the GPU
+    and quantized by the HIP kernel."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layers = []
+    for _ in range(nlayers):
+        layer = {}
+        for name, n, k in SHAPES:
+            w = torch.randn(n, k, device=dev, generator=g) * 0.02
+            qw = quantize_int8_per_channel(w) if scheme == "int8" else quantize_int4_per_group(w, 128)
+            del w
+            layer[name] = Proj(qw, n, k, scheme)
+        layers.append(layer)
+    torch.cuda.synchronize()
+    return layers
+
+
+class Sweep:
+    """All launches of one decode step at batch M, with preallocated buffers."""
+
+    def __init__(self, layers, m, dev, names=None):
+        self.names = names or [s[0] for s in SHAPES]
+        shapes = {s[0]: s for s in SHAPES}
+        self.calls = []
+        lib = _lib.load()
+        ws_bytes = 0
+        self.bytes = 0
+        self.flops = 0
+        for layer in layers:
+            for name in self.names:
+                _, n, k = shapes[name]
+                p = layer[name]
+                x = torch.randn(m, k, device=dev)
+                y = torch.empty(m, n, device=dev)
+                ws_bytes = max(ws_bytes, lib.kq_linear_workspace_bytes(
+                    8 if p.scheme == "int8" else 4, m, n, k, 128))
+                self.calls.append((p, x, y))
+                self.bytes += algorithmic_bytes(m, n, k, p.scheme)
+                self.flops += 2 * m * n * k
+        self.ws_bytes = ws_bytes
+        self.ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        self.graph = None
+
+    def run(self):
+        stream = torch.cuda.current_stream().cuda_stream
+        wsp = self.ws.data_ptr() if self.ws_bytes else None
+        for p, x, y in self.calls:
+            p.launch(x, y, wsp, self.ws_bytes, stream)
+
+    def capture(self):
+        self.run()                                   # warm the launch path outside capture
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self.run()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graph = g
+
+    def step(self):
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.run()
+
+
+def time_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps            # ms per step
+
+
+def measure(layers, m, dev, steps, warmup, eager, names=None):
+    sw = Sweep(layers, m, dev, names)
+    if not eager:
+        sw.capture()
+    ms = time_steps(sw.step, steps, warmup)
+    return {"ms": ms, "bytes": sw.bytes, "flops": sw.flops,
+            "gbs": sw.bytes / (ms * 1e-3) / 1e9, "tflops": sw.flops / (ms * 1e-3) / 1e12}
+
+
+def prefill_tflops(dev, steps, warmup, eager):
+    """Config: INT4 G=128 prefill chunk through one Llama-3-8B MLP."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    mk = lambda n, k: Proj(quantize_int4_per_group(torch.randn(n, k, device=dev, generator=g) * 0.02, 128), n, k, "int4")
+    gate, up, down = mk(14336, 4096), mk(14336, 4096), mk(4096, 14336)
+    lib = _lib.load()
+    x = torch.randn(512, 4096, device=dev)
+    a = torch.randn(512, 14336, device=dev)
+    yg, yu, yd = (torch.empty(512, 14336, device=dev), torch.empty(512, 14336, device=dev),
+                  torch.empty(512, 4096, device=dev))
+    wsb = max(lib.kq_linear_workspace_bytes(4, 512, 14336, 4096, 128),
+              lib.kq_linear_workspace_bytes(4, 512, 4096, 14336, 128))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+
+    def run():
+        st = torch.cuda.current_stream().cuda_stream
+        gate.launch(x, yg, ws.data_ptr(), wsb, st)
+        up.launch(x, yu, ws.data_ptr(), wsb, st)
+        down.launch(a, yd, ws.data_ptr(), wsb, st)
+
+    fn = run
+    if not eager:
+        run()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                run()
+        torch.cuda.current_stream().wait_stream(s)
+        fn = graph.replay
+    ms = time_steps(fn, steps, warmup)
+    flops = 3 * 2 * 512 * 14336 * 4096
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gflop": flops / 1e9}
+
+
+def cpu_baseline(layer, budget_s=20.0):
+    """The oracle's restatement of QuantizedLinear.forward (materialise the fp32
+    weight, then fp32 BLAS), on this host's cores, over one layer at M = 1."""
+    from oracle import quant
+    try:
+        from threadpoolctl import threadpool_limits, threadpool_info
+        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()
+                            if i.get("user_api") == "blas"] or [1])
+    except Exception:                                # threadpoolctl absent: report the default
+        threadpool_limits, blas_threads = None, None
+    host = []
+    for name, n, k in SHAPES:
+        p = layer[name]
+        host.append((p.qw.payload.cpu().numpy(), p.qw.scales.cpu().numpy(), n, k,
+                     np.random.default_rng(0).standard_normal((1, k)).astype(np.float32)))
+    nbytes = sum(algorithmic_bytes(1, n, k, "int4") for _, _, n, k, _ in host)
+
+    def one_pass():
+        for payload, scales, n, k, x in host:
+            w_hat = quant.np_dequantize_int4(payload, scales, k, 128)
+            quant.linear_f32(x, w_hat)
+
+    one_pass()                                       # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    cores = blas_threads or os.cpu_count()
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": int(cores), "kind": "port",
+            "sample": (f"one Llama-3-8B layer (7 projections, INT4 G=128, M=1): numpy "
+                       f"dequantize (1 thread) + OpenBLAS fp32 GEMV ({cores} threads); median of "
+                       f"{len(times)} passes, {t * 1e3:.1f} ms/layer; host {os.cpu_count()} CPUs"),
+            "ms_per_layer": t * 1e3}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--eager", action="store_true", help="launch without HIP graphs (for counters)")
+    ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
+    ap.add_argument("--layers", type=int, default=LAYERS,
+                    help="layers in the sweep (fewer only for counter runs; the headline uses 32)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: the quantized-linear path runs on a single GPU "
+              f"here (--gpus {args.gpus} requested); no multi-GPU figure is produced",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t_all = time.time()
+
+    nl = args.layers
+    int4 = build_layers("int4", dev, seed=1, nlayers=nl)
+    head = measure(int4, 1, dev, args.steps, args.warmup, args.eager)
+    print(f"# int4 M=1 sweep: {head['ms'] * 1e3:.1f} us/step, {head['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+
+    breakdown = {"int4_m1": {"gbs": round(head["gbs"], 1), "us_per_step": round(head["ms"] * 1e3, 1)}}
+    per_proj = {}
+    for name, n, k in SHAPES:                         # 32 same-shape launches per graph
+        r = measure(int4, 1, dev, args.steps, args.warmup, args.eager, names=[name])
+        per_proj[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2),
+                          "bytes_per_launch": r["bytes"] // nl}
+    breakdown["int4_m1_per_projection"] = per_proj
+    dom = max(("gate_proj", "up_proj", "down_proj"), key=lambda nm: per_proj[nm]["us_per_launch"])
+    dom_bytes = per_proj[dom]["bytes_per_launch"]
+    dom_us = per_proj[dom]["us_per_launch"]
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+
+    cpu = None
+    if not args.quick:
+        int8 = build_layers("int8", dev, seed=2, nlayers=nl)
+        r8 = measure(int8, 1, dev, args.steps, args.warmup, args.eager)
+        breakdown["int8_m1"] = {"gbs": round(r8["gbs"], 1), "us_per_step": round(r8["ms"] * 1e3, 1)}
+        per8 = {}
+        for name, n, k in SHAPES:
+            r = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[name])
+            per8[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2)}
+        breakdown["int8_m1_per_projection"] = per8
+        for m in (8, 32, 64):
+            r = measure(int8, m, dev, max(args.steps // 2, 3), 1, args.eager)
+            breakdown[f"int8_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
+                                       "us_per_step": round(r["ms"] * 1e3, 1)}
+            r = measure(int4, m, dev, max(args.steps // 2, 3), 1, args.eager)
+            breakdown[f"int4_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
+                                       "us_per_step": round(r["ms"] * 1e3, 1)}
+        del int8
+        torch.cuda.empty_cache()
+        pf = prefill_tflops(dev, max(args.steps // 2, 3), 1, args.eager)
+        breakdown["int4_prefill_m512_mlp"] = {"tflops": round(pf["tflops"], 1), "ms": round(pf["ms"], 3),
+                                              "gflop": round(pf["gflop"], 1),
+                                              "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}
+        cpu = cpu_baseline(int4[0])
+
+    # a plain 1 GiB device copy: the reference point for HBM-traffic counters
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+    out = {
+        "metric": "dequant-GEMV HBM GB/s (% of peak) at M=1 INT4/INT8; prefill GEMM TFLOPS",
+        "value": round(head["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xf32",
+        "data": "synthetic: N(0, 0.02) weights drawn on the GPU and quantized by the HIP kernel; x ~ N(0, 1)",
+        "config": {"workload": "Llama-3-8B decode step at M=1: 32 layers x (q,k,v,o,gate,up,down) "
+                               "INT4 G=128 dequant-GEMV, fp32 activations, one HIP graph per step",
+                   "layers": nl, "batch_m": 1, "scheme": "int4_per_group_g128",
+                   "launch": "eager" if args.eager else "hip_graph",
+                   "bytes_per_step": head["bytes"], "parallelism": "single_gpu"},
+        "frac_of_hbm_peak": round(head["gbs"] / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": f"skinny dequant-GEMV INT4 ({dom}, M=1)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": dom_bytes, "us_per_launch": dom_us},
+        "cpu_baseline": cpu,
+        "breakdown": breakdown,
+        "wall_s": round(time.time() - t_all, 1),
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -12,7 +12,7 @@
 //    partial sum; INT8 row scales scale the final sum.  The waves of a
 //    workgroup split K and are reduced through LDS in a fixed order
 //    (deterministic).  The activations are staged as fp16 hi/lo MFMA operands
-//    in LDS by the workgroup itself when they fit, else by stage_x_kernel into
+//    in LDS by the workgroup itself when they fit, else by stage_skinny_kernel into
 //    the caller's workspace.
 //  * gemm_kernel    (M > 16, prefill chunks / batched decode): workgroup tile
 //    BM x BN; the activation tile of each 128-column stage is copied into LDS
@@ -27,85 +27,104 @@
 namespace {
 
 // ---------------------------------------------------------------------------
-// Activation staging.  Entry (T, qd, m) = the 8 fp16 hi and 8 fp16 lo halves
-// that lane (qd, m) feeds to k-step T.  Two layouts:
-//   kLaneMajor  e = (qd * mrows + m) * pitch + T   (skinny kernel: a lane's
-//               k-steps are 16 bytes apart, so one base address serves all)
-//   kStepMajor  e = (T * 4 + qd) * mrows + m       (gemm kernel: a stage's
-//               entries for a row block are contiguous)
+// Activation staging.  An "entry" (T, qd, m) is the 8 activations of row m that
+// lane quad qd feeds to k-step T, split into fp16 hi and lo halves.
+//
+// Skinny layout (lane-major, one array): A-row r, quad qd, k-step T at
+//   index (qd * R + r) * pitch + T,   a lane's k-steps 16 bytes apart.
+//   HL mode (M <= 8): R = 2M rows; row m = hi(x[m]), row M + m = lo(x[m]).
+//     The MFMA sees hi and lo as different A rows, so one MFMA per k-step
+//     yields both partial sums (rows m and m + 8 of the output tile).
+//   split mode (M <= 16): R = M rows in two arrays (hi, lo); two MFMAs per k-step.
+// GEMM layout (step-major): index (T * 4 + qd) * mrows + m, arrays hi and lo,
+//   so one stage's entries for a row block are contiguous.
 // ---------------------------------------------------------------------------
-enum StageLayout { kLaneMajor = 0, kStepMajor = 1 };
-
 template <int BITS>
 __device__ __forceinline__ void stage_entry(const float* __restrict__ x, int64_t ldx, int64_t M,
-                                            int64_t K, int T, int qd, int64_t m,
+                                            int64_t K, int T, int qd, int64_t m, bool xvec,
                                             half8_t& hi, half8_t& lo) {
-  float v[8];
+  float raw8[8], v[8];
   const int64_t c0 = kstep_col0<BITS>(T, qd);
   if (m < M) {
-    const float* row = x + m * ldx;
+    const float* src = x + m * ldx + c0;
+    if (xvec && c0 + 8 <= K) {
+      const float4 a = reinterpret_cast<const float4*>(src)[0];
+      const float4 b = reinterpret_cast<const float4*>(src)[1];
+      raw8[0] = a.x; raw8[1] = a.y; raw8[2] = a.z; raw8[3] = a.w;
+      raw8[4] = b.x; raw8[5] = b.y; raw8[6] = b.z; raw8[7] = b.w;
+    } else {
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const int64_t col = c0 + kstep_perm<BITS>(s);
-      v[s] = col < K ? row[col] : 0.0f;
+      for (int s = 0; s < 8; s++) raw8[s] = c0 + s < K ? src[s] : 0.0f;
     }
   } else {
 #pragma unroll
-    for (int s = 0; s < 8; s++) v[s] = 0.0f;
+    for (int s = 0; s < 8; s++) raw8[s] = 0.0f;
   }
+#pragma unroll
+  for (int s = 0; s < 8; s++) v[s] = raw8[kstep_perm<BITS>(s)];
   split_hi_lo(v, hi, lo);
 }
 
-// Decompose a dense entry counter into (T, qd, m) and the layout's index.
-template <int LAYOUT>
-__device__ __forceinline__ int64_t stage_index(int64_t e, int64_t nT, int64_t mrows, int64_t pitch,
-                                               int& T, int& qd, int64_t& m) {
-  if constexpr (LAYOUT == kLaneMajor) {
-    T = (int)(e % nT);
-    const int64_t r = e / nT;
-    m = r % mrows;
-    qd = (int)(r / mrows);
-    return (qd * mrows + m) * pitch + T;
+// Skinny layout: write entry (T, qd, m).  HL: one array, rows m and M + m.
+template <bool HL>
+__device__ __forceinline__ void skinny_store(half8_t* __restrict__ a, int M, int64_t pitch,
+                                             int T, int qd, int m, half8_t hi, half8_t lo) {
+  if constexpr (HL) {
+    a[(int64_t)(qd * 2 * M + m) * pitch + T] = hi;
+    a[(int64_t)(qd * 2 * M + M + m) * pitch + T] = lo;
   } else {
-    m = e % mrows;
-    const int64_t t = e / mrows;
-    qd = (int)(t & 3);
-    T = (int)(t >> 2);
-    return e;
+    a[(int64_t)(qd * M + m) * pitch + T] = hi;
+    a[(int64_t)4 * M * pitch + (int64_t)(qd * M + m) * pitch + T] = lo;
   }
 }
 
-template <int BITS, int LAYOUT>
-__global__ __launch_bounds__(256) void stage_x_kernel(const float* __restrict__ x, int64_t ldx,
-                                                      int64_t M, int64_t K, int64_t nT,
-                                                      int64_t mrows, int64_t pitch,
-                                                      half8_t* __restrict__ xa_hi,
-                                                      half8_t* __restrict__ xa_lo) {
+template <int BITS, bool HL>
+__global__ __launch_bounds__(256) void stage_skinny_kernel(const float* __restrict__ x,
+                                                           int64_t ldx, int M, int64_t K,
+                                                           int nT, int64_t pitch, bool xvec,
+                                                           half8_t* __restrict__ a) {
+  const int64_t total = (int64_t)nT * 4 * M;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int T = (int)(e % nT);
+    const int r = (int)(e / nT);
+    const int m = r % M, qd = r / M;
+    half8_t hi, lo;
+    stage_entry<BITS>(x, ldx, M, K, T, qd, m, xvec, hi, lo);
+    skinny_store<HL>(a, M, pitch, T, qd, m, hi, lo);
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void stage_gemm_kernel(const float* __restrict__ x, int64_t ldx,
+                                                         int64_t M, int64_t K, int64_t nT,
+                                                         int64_t mrows, bool xvec,
+                                                         half8_t* __restrict__ xa_hi,
+                                                         half8_t* __restrict__ xa_lo) {
   const int64_t total = nT * 4 * mrows;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
-    int T, qd;
-    int64_t m;
-    const int64_t idx = stage_index<LAYOUT>(e, nT, mrows, pitch, T, qd, m);
+    const int64_t m = e % mrows, t = e / mrows;
     half8_t hi, lo;
-    stage_entry<BITS>(x, ldx, M, K, T, qd, m, hi, lo);
-    xa_hi[idx] = hi;
-    xa_lo[idx] = lo;
+    stage_entry<BITS>(x, ldx, M, K, (int)(t >> 2), (int)(t & 3), m, xvec, hi, lo);
+    xa_hi[e] = hi;
+    xa_lo[e] = lo;
   }
 }
 
 // ---------------------------------------------------------------------------
 // Skinny kernel: M <= 16.  grid.x = ceil(N / 16) column tiles; blockDim =
-// 64 * W, wave w owns units [w * per_wave, (w + 1) * per_wave) (unit = INT4
-// group of 128 columns / INT8 window of 64 columns), loaded KS at a time.
+// 64 * W; wave w owns units [w * per_wave, (w + 1) * per_wave) of its tile
+// (unit = INT4 group of 128 columns / INT8 window of 64 columns), loaded KS
+// at a time.  The first chunk's weight loads are issued before the
+// activations are staged, so HBM latency overlaps the staging.
 // ---------------------------------------------------------------------------
-template <int BITS, int KS, bool A_LDS>
+template <int BITS, int KS, bool A_LDS, bool HL>
 __global__ __launch_bounds__(1024) void skinny_kernel(
-    const float* __restrict__ x, int64_t ldx, int M, int64_t K,
+    const float* __restrict__ x, int64_t ldx, int M, int64_t K, bool xvec,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
-    int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa_hi,
-    const half8_t* __restrict__ xa_lo, const float* __restrict__ bias, float* __restrict__ y,
-    int64_t ldy, int64_t N) {
+    int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
+    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int TPU = BITS == 4 ? 4 : 2;  // k-steps per unit
   const int tid = threadIdx.x, lane = tid & 63;
@@ -114,36 +133,51 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
   const int qd = lane >> 4, c = lane & 15;
   const int nT = (int)(nunits * TPU);
 
-  const half8_t* a_hi = xa_hi;
-  const half8_t* a_lo = xa_lo;
-  if constexpr (A_LDS) {
-    half8_t* l_hi = reinterpret_cast<half8_t*>(smem);
-    half8_t* l_lo = l_hi + 4 * M * pitch;
-    const int entries = nT * 4 * M;
-    for (int e = tid; e < entries; e += blockDim.x) {
-      int T, q4;
-      int64_t m;
-      const int idx = (int)stage_index<kLaneMajor>(e, nT, M, pitch, T, q4, m);
-      half8_t hi, lo;
-      stage_entry<BITS>(x, ldx, M, K, T, q4, m, hi, lo);
-      l_hi[idx] = hi;
-      l_lo[idx] = lo;
-    }
-    __syncthreads();
-    a_hi = l_hi;
-    a_lo = l_lo;
-  }
-  // This lane's activation entries: k-step T at a_*_lane[T].
-  const int a_row = c < M ? c : 0;
-  const half8_t* a_hi_lane = a_hi + (int64_t)(qd * M + a_row) * pitch;
-  const half8_t* a_lo_lane = a_lo + (int64_t)(qd * M + a_row) * pitch;
-
   const int64_t n = (int64_t)blockIdx.x * 16 + c;
   const int64_t nl = n < N ? n : N - 1;
   const uint8_t* wrow = wq + nl * row_bytes + qd * 16;
   const int64_t ub = (int64_t)wave * per_wave;
   const int64_t ue = ub + per_wave < nunits ? ub + per_wave : nunits;
-  const bool a_lane = c < M;  // lanes holding activation row c; the rest stay zero
+
+  // First chunk in flight before anything else.
+  u32x4 raw[KS];
+  if (ub < ue) {
+#pragma unroll
+    for (int u = 0; u < KS; u++) {
+      const int64_t unit = ub + u < ue ? ub + u : ue - 1;  // tail: reload the last unit, unused
+      raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
+    }
+  }
+
+  const half8_t* a = xa;
+  if constexpr (A_LDS) {
+    half8_t* la = reinterpret_cast<half8_t*>(smem);
+    const int entries = nT * 4 * M;
+    for (int e = tid; e < entries; e += blockDim.x) {
+      const int T = e % nT, r = e / nT;
+      const int m = r % M, q4 = r / M;
+      half8_t hi, lo;
+      stage_entry<BITS>(x, ldx, M, K, T, q4, m, xvec, hi, lo);
+      skinny_store<HL>(la, M, pitch, T, q4, m, hi, lo);
+    }
+    __syncthreads();
+    a = la;
+  }
+
+  // This lane's activation operand: A-row c of the MFMA.
+  bool a_lane;
+  const half8_t* a_hi_lane;
+  const half8_t* a_lo_lane;
+  if constexpr (HL) {
+    const int r = c < M ? c : (c >= 8 && c < 8 + M) ? M + c - 8 : -1;
+    a_lane = r >= 0;
+    a_hi_lane = a + (int64_t)(qd * 2 * M + (a_lane ? r : 0)) * pitch;
+    a_lo_lane = a_hi_lane;
+  } else {
+    a_lane = c < M;
+    a_hi_lane = a + (int64_t)(qd * M + (a_lane ? c : 0)) * pitch;
+    a_lo_lane = a_hi_lane + (int64_t)4 * M * pitch;
+  }
 
   floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   half8_t ah[TPU], al[TPU];
@@ -151,11 +185,12 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
   for (int i = 0; i < TPU; i++) { ah[i] = half8_t{}; al[i] = half8_t{}; }
 
   for (int64_t u0 = ub; u0 < ue; u0 += KS) {
-    u32x4 raw[KS];
+    if (u0 != ub) {
 #pragma unroll
-    for (int u = 0; u < KS; u++) {
-      const int64_t unit = u0 + u < ue ? u0 + u : ue - 1;  // tail: reload the last unit, unused
-      raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
+      for (int u = 0; u < KS; u++) {
+        const int64_t unit = u0 + u < ue ? u0 + u : ue - 1;
+        raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
+      }
     }
 #pragma unroll
     for (int u = 0; u < KS; u++) {
@@ -165,7 +200,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
 #pragma unroll
           for (int i = 0; i < TPU; i++) {
             ah[i] = a_hi_lane[unit * TPU + i];
-            al[i] = a_lo_lane[unit * TPU + i];
+            if constexpr (!HL) al[i] = a_lo_lane[unit * TPU + i];
           }
         }
         if constexpr (BITS == 4) {
@@ -175,7 +210,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
           for (int i = 0; i < 4; i++) {
             const half8_t b = int4x8_to_half8(raw[u][i]);
             g = mfma16x16x32(ah[i], b, g);
-            g = mfma16x16x32(al[i], b, g);
+            if constexpr (!HL) g = mfma16x16x32(al[i], b, g);
           }
 #pragma unroll
           for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(s, g[i], acc[i]);
@@ -184,7 +219,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
           for (int j = 0; j < 2; j++) {
             const half8_t b = int8x8_to_half8(raw[u][2 * j], raw[u][2 * j + 1]);
             acc = mfma16x16x32(ah[j], b, acc);
-            acc = mfma16x16x32(al[j], b, acc);
+            if constexpr (!HL) acc = mfma16x16x32(al[j], b, acc);
           }
         }
       }
@@ -194,7 +229,8 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
     }
   }
 
-  // Cross-wave reduction in a fixed order.  Lane (qd, c) holds rows 4qd+i, column c.
+  // Cross-wave reduction in a fixed order.  Lane (qd, c) holds output-tile
+  // rows 4qd+i, column c (HL: row m is the hi part of x[m], row m + 8 its lo part).
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
@@ -205,7 +241,10 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
     const int64_t nn = (int64_t)blockIdx.x * 16 + cc;
     if (nn < N) {
       float v = 0.0f;
-      for (int w = 0; w < nwaves; w++) v += red[(w * 16 + m) * 16 + cc];
+      for (int w = 0; w < nwaves; w++) {
+        v += red[(w * 16 + m) * 16 + cc];
+        if constexpr (HL) v += red[(w * 16 + m + 8) * 16 + cc];
+      }
       if constexpr (BITS == 8) v *= f16_bits_to_f32(sc[nn]);
       if (bias) v += bias[nn];
       y[m * ldy + nn] = v;
@@ -372,8 +411,10 @@ __global__ __launch_bounds__(256) void generic_kernel(const float* __restrict__ 
 // Host dispatch
 // ---------------------------------------------------------------------------
 constexpr int kSkinnyMaxM = 16;
+constexpr int kSkinnyHLMaxM = 8;             // hi/lo in separate MFMA rows up to M = 8
 constexpr int kSkinnyMaxWaves = 16;
-constexpr int64_t kSkinnyLdsA = 64 * 1024;  // activation bytes staged in LDS by the workgroup
+constexpr int64_t kSkinnyTargetWaves = 3072; // ~12 waves per CU across 256 CUs
+constexpr int64_t kSkinnyLdsA = 64 * 1024;   // activation bytes staged in LDS by the workgroup
 constexpr int kGemmMTW = 4, kGemmNTW = 4, kGemmWN = 4;
 constexpr int64_t kGemmBM = 16 * kGemmMTW;
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
@@ -382,14 +423,15 @@ enum class Path { Skinny, Gemm, Generic };
 
 struct Plan {
   Path path;
-  int ks = 0;           // skinny: units per wave
+  int ks = 0;           // skinny: units per load batch (template)
   int waves = 0;        // skinny: waves per workgroup
-  int64_t per_wave = 0; // skinny: units per wave (processed KS at a time)
-  bool a_lds = false;   // skinny: activations staged in LDS
+  int64_t per_wave = 0; // skinny: units per wave
+  bool a_lds = false;   // skinny: activations staged in LDS by the workgroup
+  bool hl = false;      // skinny: hi/lo halves in separate MFMA rows
   int64_t nunits = 0;   // INT4 groups / INT8 windows per row
   int64_t nT = 0;       // k-steps
-  int64_t mrows = 0;    // staged activation rows
-  int64_t pitch = 0;    // skinny: entries per (quad, row) in the lane-major layout
+  int64_t mrows = 0;    // staged activation rows (gemm)
+  int64_t pitch = 0;    // skinny: entries per (quad, A-row) in the lane-major layout
   size_t ws = 0;        // workspace bytes
 };
 
@@ -400,16 +442,20 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   p.nunits = bits == 4 ? kp / 128 : k / 64;
   p.nT = p.nunits * (bits == 4 ? 4 : 2);
   if (m <= kSkinnyMaxM) {
-    int ks = 4;
-    while (ks < 16 && (p.nunits + ks - 1) / ks > kSkinnyMaxWaves) ks *= 2;
     p.path = Path::Skinny;
-    p.ks = ks;
-    p.waves = (int)std::min<int64_t>((p.nunits + ks - 1) / ks, kSkinnyMaxWaves);
-    p.per_wave = (p.nunits + p.waves - 1) / p.waves;
-    p.mrows = m;
+    p.hl = m <= kSkinnyHLMaxM;
+    // Waves per workgroup: enough workgroup-waves in total to keep ~12 waves
+    // per CU streaming, each wave an equal share of the tile's K units.
+    const int64_t ntiles = (n + 15) / 16;
+    int64_t w = (kSkinnyTargetWaves + ntiles - 1) / ntiles;
+    w = std::max<int64_t>(1, std::min<int64_t>(w, kSkinnyMaxWaves));
+    w = std::min(w, p.nunits);
+    p.per_wave = (p.nunits + w - 1) / w;
+    p.waves = (int)((p.nunits + p.per_wave - 1) / p.per_wave);
+    p.ks = p.per_wave <= 2 ? 2 : p.per_wave <= 4 ? 4 : p.per_wave <= 8 ? 8 : 16;
     // An odd pitch puts the four lane quads of an LDS row in different banks.
     p.pitch = p.nT | 1;
-    p.a_lds = 128 * p.pitch * m <= kSkinnyLdsA;  // 2 planes x 16 B x 4 quads per entry
+    p.a_lds = 128 * p.pitch * m <= kSkinnyLdsA;  // 2 halves x 16 B x 4 quads per entry
     if (!p.a_lds) p.pitch = p.nT;
     p.ws = p.a_lds ? 0 : (size_t)(128 * p.pitch * m);
     return p;
@@ -423,45 +469,57 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   return p;
 }
 
+inline bool x_vectorizable(const float* x, int64_t ldx) {
+  return (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 4 == 0);
+}
+
+template <int BITS, bool LDS, bool HL>
+void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStream_t st,
+                      const float* x, int64_t ldx, int64_t m, int64_t k, bool xvec,
+                      const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
+                      const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n) {
+#define KQ_SKINNY(KS_)                                                                           \
+  skinny_kernel<BITS, KS_, LDS, HL><<<grid, block, shm, st>>>(x, ldx, (int)m, k, xvec, wq, sc, \
+                                                              row_bytes, ng, p.nunits,         \
+                                                              p.per_wave, (int)p.pitch, xa,    \
+                                                              bias, y, ldy, n)
+  switch (p.ks) {
+    case 2: KQ_SKINNY(2); break;
+    case 4: KQ_SKINNY(4); break;
+    case 8: KQ_SKINNY(8); break;
+    default: KQ_SKINNY(16); break;
+  }
+#undef KQ_SKINNY
+}
+
 template <int BITS>
 int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k,
                   const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                   const float* bias, float* y, int64_t ldy, int64_t n, void* ws, hipStream_t st) {
-  const half8_t* xh = nullptr;
-  const half8_t* xl = nullptr;
+  const bool xvec = x_vectorizable(x, ldx);
+  const half8_t* xa = nullptr;
   if (!p.a_lds) {
-    half8_t* h = static_cast<half8_t*>(ws);
-    half8_t* l = h + p.pitch * 4 * m;  // planes of 4 * m * pitch entries
+    half8_t* a = static_cast<half8_t*>(ws);
     const int64_t entries = p.nT * 4 * m;
-    unsigned grid = (unsigned)std::min<int64_t>((entries + 255) / 256, 4096);
-    stage_x_kernel<BITS, kLaneMajor><<<grid, 256, 0, st>>>(x, ldx, m, k, p.nT, m, p.pitch, h, l);
-    xh = h;
-    xl = l;
+    const unsigned sg = (unsigned)std::min<int64_t>((entries + 255) / 256, 4096);
+    if (p.hl)
+      stage_skinny_kernel<BITS, true><<<sg, 256, 0, st>>>(x, ldx, (int)m, k, (int)p.nT, p.pitch, xvec, a);
+    else
+      stage_skinny_kernel<BITS, false><<<sg, 256, 0, st>>>(x, ldx, (int)m, k, (int)p.nT, p.pitch, xvec, a);
+    xa = a;
   }
   const size_t red = (size_t)p.waves * 256 * sizeof(float);
-  const size_t a = p.a_lds ? (size_t)(4 * p.pitch * 32 * m) : 0;
-  const size_t shm = std::max(red, a);
+  const size_t abytes = p.a_lds ? (size_t)(128 * p.pitch * m) : 0;
+  const size_t shm = std::max(red, abytes);
   const dim3 grid((unsigned)((n + 15) / 16));
   const dim3 block((unsigned)(64 * p.waves));
-#define KQ_SKINNY(KS_, LDS_)                                                                  \
-  skinny_kernel<BITS, KS_, LDS_><<<grid, block, shm, st>>>(x, ldx, (int)m, k, wq, sc,       \
-                                                           row_bytes, ng, p.nunits,         \
-                                                           p.per_wave, (int)p.pitch, xh, xl, \
-                                                           bias, y, ldy, n)
   if (p.a_lds) {
-    switch (p.ks) {
-      case 4: KQ_SKINNY(4, true); break;
-      case 8: KQ_SKINNY(8, true); break;
-      default: KQ_SKINNY(16, true); break;
-    }
+    if (p.hl) launch_skinny_ks<BITS, true, true>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
+    else launch_skinny_ks<BITS, true, false>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
   } else {
-    switch (p.ks) {
-      case 4: KQ_SKINNY(4, false); break;
-      case 8: KQ_SKINNY(8, false); break;
-      default: KQ_SKINNY(16, false); break;
-    }
+    if (p.hl) launch_skinny_ks<BITS, false, true>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
+    else launch_skinny_ks<BITS, false, false>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
   }
-#undef KQ_SKINNY
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }
 
@@ -473,7 +531,8 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
   half8_t* l = h + p.nT * 4 * p.mrows;
   const int64_t entries = p.nT * 4 * p.mrows;
   unsigned sgrid = (unsigned)std::min<int64_t>((entries + 255) / 256, 8192);
-  stage_x_kernel<BITS, kStepMajor><<<sgrid, 256, 0, st>>>(x, ldx, m, k, p.nT, p.mrows, 0, h, l);
+  stage_gemm_kernel<BITS><<<sgrid, 256, 0, st>>>(x, ldx, m, k, p.nT, p.mrows,
+                                                 x_vectorizable(x, ldx), h, l);
   const dim3 grid((unsigned)((n + kGemmBN - 1) / kGemmBN), (unsigned)(p.mrows / kGemmBM));
   gemm_kernel<BITS, kGemmMTW, kGemmNTW, kGemmWN><<<grid, 64 * kGemmWN, 0, st>>>(
       h, l, p.mrows, wq, sc, row_bytes, ng, p.nT / 4, bias, y, ldy, m, n);
