@@ -39,11 +39,11 @@ namespace {
 // GEMM layout (step-major): index (T * 4 + qd) * mrows + m, arrays hi and lo,
 //   so one stage's entries for a row block are contiguous.
 // ---------------------------------------------------------------------------
+// Load the 8 consecutive activations of entry (T, qd, m) (zeros past M / K).
 template <int BITS>
-__device__ __forceinline__ void stage_entry(const float* __restrict__ x, int64_t ldx, int64_t M,
-                                            int64_t K, int T, int qd, int64_t m, bool xvec,
-                                            half8_t& hi, half8_t& lo) {
-  float raw8[8], v[8];
+__device__ __forceinline__ void stage_load(const float* __restrict__ x, int64_t ldx, int64_t M,
+                                           int64_t K, int T, int qd, int64_t m, bool xvec,
+                                           float (&raw8)[8]) {
   const int64_t c0 = kstep_col0<BITS>(T, qd);
   if (m < M) {
     const float* src = x + m * ldx + c0;
@@ -60,9 +60,24 @@ __device__ __forceinline__ void stage_entry(const float* __restrict__ x, int64_t
 #pragma unroll
     for (int s = 0; s < 8; s++) raw8[s] = 0.0f;
   }
+}
+
+// Permute the 8 loaded activations into operand-slot order and split them.
+template <int BITS>
+__device__ __forceinline__ void stage_convert(const float (&raw8)[8], half8_t& hi, half8_t& lo) {
+  float v[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) v[s] = raw8[kstep_perm<BITS>(s)];
   split_hi_lo(v, hi, lo);
+}
+
+template <int BITS>
+__device__ __forceinline__ void stage_entry(const float* __restrict__ x, int64_t ldx, int64_t M,
+                                            int64_t K, int T, int qd, int64_t m, bool xvec,
+                                            half8_t& hi, half8_t& lo) {
+  float raw8[8];
+  stage_load<BITS>(x, ldx, M, K, T, qd, m, xvec, raw8);
+  stage_convert<BITS>(raw8, hi, lo);
 }
 
 // Skinny layout: write entry (T, qd, m).  HL: one array, rows m and M + m.
@@ -112,6 +127,39 @@ __global__ __launch_bounds__(256) void stage_gemm_kernel(const float* __restrict
   }
 }
 
+// Group scales of units [u0, u0 + KS) of one row.  SVEC: one vector load of
+// the KS consecutive fp16 scales (row and u0 aligned to KS), so a wave issues
+// one load per row for KS units instead of KS loads; else one load per unit,
+// clamped to the last valid unit.
+template <int KS, bool SVEC>
+__device__ __forceinline__ void load_scales(const uint16_t* __restrict__ srow, int64_t u0,
+                                            int64_t ue, uint16_t (&sv)[KS]) {
+  if constexpr (SVEC) {
+    const uint16_t* p = srow + u0;
+    if constexpr (KS == 2) {
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+      sv[0] = (uint16_t)v; sv[1] = (uint16_t)(v >> 16);
+    } else {
+#pragma unroll
+      for (int h = 0; h < KS / 8 + (KS < 8); h++) {
+        if constexpr (KS == 4) {
+          const uint2 v = *reinterpret_cast<const uint2*>(p);
+          const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+          for (int i = 0; i < 4; i++) sv[i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+        } else {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(p + 8 * h);
+#pragma unroll
+          for (int i = 0; i < 8; i++) sv[8 * h + i] = (uint16_t)(v[i >> 1] >> (16 * (i & 1)));
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < KS; u++) sv[u] = srow[u0 + u < ue ? u0 + u : ue - 1];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Skinny kernel: M <= 16.  grid.x = ceil(N / 16) column tiles; blockDim =
 // 64 * W; wave w owns units [w * per_wave, (w + 1) * per_wave) of its tile
@@ -119,7 +167,7 @@ __global__ __launch_bounds__(256) void stage_gemm_kernel(const float* __restrict
 // at a time.  The first chunk's weight loads are issued before the
 // activations are staged, so HBM latency overlaps the staging.
 // ---------------------------------------------------------------------------
-template <int BITS, int KS, bool A_LDS, bool HL>
+template <int BITS, int KS, bool A_LDS, bool HL, bool SVEC>
 __global__ __launch_bounds__(1024) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int64_t K, bool xvec,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
@@ -139,26 +187,71 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
   const int64_t ub = (int64_t)wave * per_wave;
   const int64_t ue = ub + per_wave < nunits ? ub + per_wave : nunits;
 
-  // First chunk in flight before anything else.
-  u32x4 raw[KS];
-  if (ub < ue) {
+  // Vector-memory counters retire in issue order, so the activation loads of
+  // the staging are issued first: waiting for them does not wait for the
+  // weights.  Then the first chunk of packed weights (and, for INT4, its group
+  // scales) goes in flight, then the staging converts while HBM answers.
+  // Staging work split without integer division: thread (wave, lane) owns
+  // k-steps T = wave * 64 + lane + j * 64 * W and stages all 4 * M rows of
+  // each.  The first of them (rows m = 0 of the 4 quads; all of M = 1) is
+  // loaded before the weights.
+  const int t0 = wave * 64 + lane;
+  const int tstride = nwaves * 64;
+  float4 xa4[4], xb4[4];
+  bool pre_ok = false;
+  if constexpr (A_LDS) {
+    // All four quads' 8 columns must lie inside the row (quad 3 ends last).
+    pre_ok = xvec && t0 < nT && kstep_col0<BITS>(t0, 3) + 8 <= K;
+    const int tl = pre_ok ? t0 : 0;
 #pragma unroll
-    for (int u = 0; u < KS; u++) {
-      const int64_t unit = ub + u < ue ? ub + u : ue - 1;  // tail: reload the last unit, unused
-      raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
+    for (int q4 = 0; q4 < 4; q4++) {
+      const float* src = x + (pre_ok ? kstep_col0<BITS>(tl, q4) : 0);
+      xa4[q4] = reinterpret_cast<const float4*>(src)[0];
+      xb4[q4] = reinterpret_cast<const float4*>(src)[1];
     }
   }
+  // Keep these loads ahead of the weight loads (an IR-level ordering fence;
+  // it emits no instruction and no wait).
+  __asm__ volatile("" ::: "memory");
+
+  const uint16_t* srow = sc + nl * ng;
+  u32x4 raw[KS];
+  uint16_t sv[KS];  // raw fp16 bits: converting at load time would force an early wait
+  // Unconditional (a branch here would make every later wait conservative):
+  // units past ue reload unit ue - 1, which is in [0, nunits) for every wave.
+#pragma unroll
+  for (int u = 0; u < KS; u++) {
+    const int64_t unit = ub + u < ue ? ub + u : ue - 1;
+    raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
+  }
+  if constexpr (BITS == 4) load_scales<KS, SVEC>(srow, ub, ue, sv);
 
   const half8_t* a = xa;
   if constexpr (A_LDS) {
     half8_t* la = reinterpret_cast<half8_t*>(smem);
-    const int entries = nT * 4 * M;
-    for (int e = tid; e < entries; e += blockDim.x) {
-      const int T = e % nT, r = e / nT;
-      const int m = r % M, q4 = r / M;
+    // Unconditional: a thread without a valid pre-load writes its (unused)
+    // values to the pad column T = nT, which no lane reads.  A branch here
+    // would let the compiler sink the pre-loads behind the weight loads.
+    const int tp = pre_ok ? t0 : nT;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; q4++) {
+      const float raw8[8] = {xa4[q4].x, xa4[q4].y, xa4[q4].z, xa4[q4].w,
+                             xb4[q4].x, xb4[q4].y, xb4[q4].z, xb4[q4].w};
       half8_t hi, lo;
-      stage_entry<BITS>(x, ldx, M, K, T, q4, m, xvec, hi, lo);
-      skinny_store<HL>(la, M, pitch, T, q4, m, hi, lo);
+      stage_convert<BITS>(raw8, hi, lo);
+      skinny_store<HL>(la, M, pitch, tp, q4, 0, hi, lo);
+    }
+    // Everything else (rows m > 0, further k-steps, unaligned x): loaded now,
+    // after the weights are in flight.
+    for (int T = t0; T < nT; T += tstride) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) {
+        for (int m = (T == t0 && pre_ok) ? 1 : 0; m < M; m++) {
+          half8_t hi, lo;
+          stage_entry<BITS>(x, ldx, M, K, T, q4, m, xvec, hi, lo);
+          skinny_store<HL>(la, M, pitch, T, q4, m, hi, lo);
+        }
+      }
     }
     __syncthreads();
     a = la;
@@ -191,6 +284,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
         const int64_t unit = u0 + u < ue ? u0 + u : ue - 1;
         raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
       }
+      if constexpr (BITS == 4) load_scales<KS, SVEC>(srow, u0, ue, sv);
     }
 #pragma unroll
     for (int u = 0; u < KS; u++) {
@@ -204,7 +298,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
           }
         }
         if constexpr (BITS == 4) {
-          const float s = f16_bits_to_f32(sc[nl * ng + unit]);
+          const float s = f16_bits_to_f32(sv[u]);
           floatx4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int i = 0; i < 4; i++) {
@@ -428,6 +522,7 @@ struct Plan {
   int64_t per_wave = 0; // skinny: units per wave
   bool a_lds = false;   // skinny: activations staged in LDS by the workgroup
   bool hl = false;      // skinny: hi/lo halves in separate MFMA rows
+  bool svec = false;    // skinny INT4: vector loads of KS consecutive group scales
   int64_t nunits = 0;   // INT4 groups / INT8 windows per row
   int64_t nT = 0;       // k-steps
   int64_t mrows = 0;    // staged activation rows (gemm)
@@ -444,17 +539,28 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   if (m <= kSkinnyMaxM) {
     p.path = Path::Skinny;
     p.hl = m <= kSkinnyHLMaxM;
-    // Waves per workgroup: enough workgroup-waves in total to keep ~12 waves
-    // per CU streaming, each wave an equal share of the tile's K units.
+    // Units per wave: a power of two (so every wave's first unit is aligned for
+    // vector scale loads) chosen to bring the total number of waves closest
+    // to ~12 per CU, with at most 16 waves per workgroup.
     const int64_t ntiles = (n + 15) / 16;
-    int64_t w = (kSkinnyTargetWaves + ntiles - 1) / ntiles;
-    w = std::max<int64_t>(1, std::min<int64_t>(w, kSkinnyMaxWaves));
-    w = std::min(w, p.nunits);
-    p.per_wave = (p.nunits + w - 1) / w;
-    p.waves = (int)((p.nunits + p.per_wave - 1) / p.per_wave);
-    p.ks = p.per_wave <= 2 ? 2 : p.per_wave <= 4 ? 4 : p.per_wave <= 8 ? 8 : 16;
-    // An odd pitch puts the four lane quads of an LDS row in different banks.
-    p.pitch = p.nT | 1;
+    int64_t best_pw = 16;
+    double best = 1e30;
+    for (int64_t pw = 2; pw <= 16; pw *= 2) {
+      const int64_t w = (p.nunits + pw - 1) / pw;
+      if (w > kSkinnyMaxWaves) continue;
+      const double r = (double)(ntiles * w) / (double)kSkinnyTargetWaves;
+      const double score = r >= 1.0 ? r : 1.0 / r;
+      if (score < best) { best = score; best_pw = pw; }
+    }
+    p.per_wave = best_pw;
+    p.waves = (int)std::min<int64_t>((p.nunits + best_pw - 1) / best_pw, kSkinnyMaxWaves);
+    if ((int64_t)p.waves * best_pw < p.nunits)          // K beyond 16 x 16 units: KS-unit chunks
+      p.per_wave = (p.nunits + p.waves - 1) / p.waves;
+    p.ks = (int)std::min<int64_t>(best_pw, 16);
+    p.svec = bits == 4 && p.per_wave % p.ks == 0 && (kp / 128) % p.ks == 0;
+    // An odd pitch puts the four lane quads of an LDS row in different banks;
+    // column nT is a pad column (written with unused values, never read).
+    p.pitch = (p.nT + 1) | 1;
     p.a_lds = 128 * p.pitch * m <= kSkinnyLdsA;  // 2 halves x 16 B x 4 quads per entry
     if (!p.a_lds) p.pitch = p.nT;
     p.ws = p.a_lds ? 0 : (size_t)(128 * p.pitch * m);
@@ -469,17 +575,17 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   return p;
 }
 
-inline bool x_vectorizable(const float* x, int64_t ldx) {
-  return (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 4 == 0);
+inline bool x_vectorizable(const float* x, int64_t ldx, int64_t k) {
+  return (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 4 == 0) && k >= 8;
 }
 
-template <int BITS, bool LDS, bool HL>
+template <int BITS, bool LDS, bool HL, bool SVEC>
 void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStream_t st,
                       const float* x, int64_t ldx, int64_t m, int64_t k, bool xvec,
                       const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                       const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n) {
 #define KQ_SKINNY(KS_)                                                                           \
-  skinny_kernel<BITS, KS_, LDS, HL><<<grid, block, shm, st>>>(x, ldx, (int)m, k, xvec, wq, sc, \
+  skinny_kernel<BITS, KS_, LDS, HL, SVEC><<<grid, block, shm, st>>>(x, ldx, (int)m, k, xvec, wq, sc, \
                                                               row_bytes, ng, p.nunits,         \
                                                               p.per_wave, (int)p.pitch, xa,    \
                                                               bias, y, ldy, n)
@@ -496,7 +602,7 @@ template <int BITS>
 int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k,
                   const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                   const float* bias, float* y, int64_t ldy, int64_t n, void* ws, hipStream_t st) {
-  const bool xvec = x_vectorizable(x, ldx);
+  const bool xvec = x_vectorizable(x, ldx, k);
   const half8_t* xa = nullptr;
   if (!p.a_lds) {
     half8_t* a = static_cast<half8_t*>(ws);
@@ -513,13 +619,23 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   const size_t shm = std::max(red, abytes);
   const dim3 grid((unsigned)((n + 15) / 16));
   const dim3 block((unsigned)(64 * p.waves));
+  const bool svec = p.svec && reinterpret_cast<uintptr_t>(sc) % (2 * p.ks) == 0;
+#define KQ_SKINNY_SV(LDS_, HL_)                                                                 \
+  do {                                                                                          \
+    if (svec) launch_skinny_ks<BITS, LDS_, HL_, true>(p, grid, block, shm, st, x, ldx, m, k,   \
+                                                      xvec, wq, sc, row_bytes, ng, xa, bias, y, \
+                                                      ldy, n);                                  \
+    else launch_skinny_ks<BITS, LDS_, HL_, false>(p, grid, block, shm, st, x, ldx, m, k, xvec,  \
+                                                  wq, sc, row_bytes, ng, xa, bias, y, ldy, n);  \
+  } while (0)
   if (p.a_lds) {
-    if (p.hl) launch_skinny_ks<BITS, true, true>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
-    else launch_skinny_ks<BITS, true, false>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
+    if (p.hl) KQ_SKINNY_SV(true, true);
+    else KQ_SKINNY_SV(true, false);
   } else {
-    if (p.hl) launch_skinny_ks<BITS, false, true>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
-    else launch_skinny_ks<BITS, false, false>(p, grid, block, shm, st, x, ldx, m, k, xvec, wq, sc, row_bytes, ng, xa, bias, y, ldy, n);
+    if (p.hl) KQ_SKINNY_SV(false, true);
+    else KQ_SKINNY_SV(false, false);
   }
+#undef KQ_SKINNY_SV
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }
 
@@ -532,7 +648,7 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
   const int64_t entries = p.nT * 4 * p.mrows;
   unsigned sgrid = (unsigned)std::min<int64_t>((entries + 255) / 256, 8192);
   stage_gemm_kernel<BITS><<<sgrid, 256, 0, st>>>(x, ldx, m, k, p.nT, p.mrows,
-                                                 x_vectorizable(x, ldx), h, l);
+                                                 x_vectorizable(x, ldx, k), h, l);
   const dim3 grid((unsigned)((n + kGemmBN - 1) / kGemmBN), (unsigned)(p.mrows / kGemmBM));
   gemm_kernel<BITS, kGemmMTW, kGemmNTW, kGemmWN><<<grid, 64 * kGemmWN, 0, st>>>(
       h, l, p.mrows, wq, sc, row_bytes, ng, p.nT / 4, bias, y, ldy, m, n);
