@@ -41,6 +41,9 @@ from kshipra_amd import _lib  # noqa: E402
 from kshipra_amd.quantization import quantize_int4_per_group, quantize_int8_per_channel  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE counter passes
+# (calibrated against a 1 GiB device copy), written next to the profile summary.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "skinny_gemv_int4_llama3_8b_m1.json")
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 LAYERS = 32
 SHAPES = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096),
@@ -277,6 +280,11 @@ def main():
     dom_bytes = per_proj[dom]["bytes_per_launch"]
     dom_us = per_proj[dom]["us_per_launch"]
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    traffic, traffic_src = None, None
+    if os.path.exists(TRAFFIC_FILE):
+        tf = json.load(open(TRAFFIC_FILE))
+        traffic = tf.get("hbm_bytes_per_launch", {}).get(dom)
+        traffic_src = tf.get("source") if traffic is not None else None
 
     cpu = None
     if not args.quick:
@@ -330,7 +338,8 @@ def main():
         "frac_of_hbm_peak": round(head["gbs"] / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "kernel": f"skinny dequant-GEMV INT4 ({dom}, M=1)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "bytes_per_launch": dom_bytes, "us_per_launch": dom_us},
         "cpu_baseline": cpu,
         "breakdown": breakdown,
