@@ -15,9 +15,11 @@
 //    in LDS by the workgroup itself when they fit, else by stage_skinny_kernel into
 //    the caller's workspace.
 //  * gemm_kernel    (M > 16, prefill chunks / batched decode): workgroup tile
-//    BM x BN; the activation tile of each 128-column stage is copied into LDS
-//    and shared by the waves, each wave streams its own weight columns from
-//    HBM into registers.
+//    BM x 256; x is converted once per call into fp16 hi/lo operand planes
+//    (stage_planes_kernel), each 128-column stage of them is copied into LDS
+//    (double-buffered) and shared by the waves; each wave streams its own
+//    weight columns from HBM into registers one stage ahead.  K is split across workgroups when the tiles alone cannot
+//    fill the GPU; partials are then added in a fixed order.
 //  * generic_kernel (any group size / K): scalar dequant + FMA fallback for
 //    shapes the MFMA paths do not tile.
 #include <algorithm>
@@ -36,8 +38,7 @@ namespace {
 //     The MFMA sees hi and lo as different A rows, so one MFMA per k-step
 //     yields both partial sums (rows m and m + 8 of the output tile).
 //   split mode (M <= 16): R = M rows in two arrays (hi, lo); two MFMAs per k-step.
-// GEMM layout (step-major): index (T * 4 + qd) * mrows + m, arrays hi and lo,
-//   so one stage's entries for a row block are contiguous.
+// GEMM operand planes: see stage_planes_kernel.
 // ---------------------------------------------------------------------------
 // Load the 8 consecutive activations of entry (T, qd, m) (zeros past M / K).
 template <int BITS>
@@ -107,23 +108,6 @@ __global__ __launch_bounds__(256) void stage_skinny_kernel(const float* __restri
     half8_t hi, lo;
     stage_entry<BITS>(x, ldx, M, K, T, qd, m, xvec, hi, lo);
     skinny_store<HL>(a, M, pitch, T, qd, m, hi, lo);
-  }
-}
-
-template <int BITS>
-__global__ __launch_bounds__(256) void stage_gemm_kernel(const float* __restrict__ x, int64_t ldx,
-                                                         int64_t M, int64_t K, int64_t nT,
-                                                         int64_t mrows, bool xvec,
-                                                         half8_t* __restrict__ xa_hi,
-                                                         half8_t* __restrict__ xa_lo) {
-  const int64_t total = nT * 4 * mrows;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t m = e % mrows, t = e / mrows;
-    half8_t hi, lo;
-    stage_entry<BITS>(x, ldx, M, K, (int)(t >> 2), (int)(t & 3), m, xvec, hi, lo);
-    xa_hi[e] = hi;
-    xa_lo[e] = lo;
   }
 }
 
@@ -347,36 +331,124 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMM kernel: M > 16.  Workgroup = WN waves along N; tile BM = 16 * MTW rows
-// by BN = 16 * NTW * WN columns; one stage = 128 columns of K (4 k-steps).
-// Activation entries come from the staged workspace (mrows = M rounded up to
-// BM, zero rows past M).
+// GEMM path: M > 16 (batched decode, prefill chunks).
+//
+// stage_planes_kernel converts x once per call into fp16 hi/lo MFMA operand
+// planes in the workspace:  entry (plane p, stage st, row m, e) at
+//   ((p * nstages + st) * Mp + m) * 16 + e        (16-byte units)
+// where stage st covers K columns [128 st, 128 st + 128), e = T * 4 + qd names
+// the 8 columns lane quad qd feeds to k-step T of the stage (already permuted
+// into operand-slot order), Mp is M rounded up to the row tile, and rows past
+// M / columns past K are zeros.
+//
+// gemm_kernel: workgroup = WN waves side by side along N; wave tile 16*MTW
+// rows x 16*NTW columns, so the workgroup tile is BM = 16*MTW by
+// BN = 16*NTW*WN.  Per stage the workgroup copies the BM x 128 operand block
+// (both planes) into LDS (double-buffered, one barrier per stage) and every
+// wave streams its own weight columns from HBM into registers.  The next
+// stage's operands, weights and scales are loaded before the current stage's
+// MFMAs so their latency hides behind the math.
+//
+// LDS layout per buffer and plane: row mm holds entry e of activation row
+// m0 + mm at mm*16 + (e ^ (mm & 15)).  The XOR makes the 16 rows an MFMA
+// operand read touches fall in distinct banks; a thread copies staged entry
+// q of the block to LDS entry q (consecutive lanes, consecutive addresses).
+//
+// Split-K: blockIdx decomposes into (m-tile, n-tile, z); split z covers
+// stages [z*spz, (z+1)*spz).  With one split the epilogue writes y; with more
+// it writes fp32 partials and splitk_reduce_kernel adds them in z order
+// (deterministic).
 // ---------------------------------------------------------------------------
+template <int BITS>
+__global__ __launch_bounds__(256) void stage_planes_kernel(const float* __restrict__ x, int64_t ldx,
+                                                           int64_t M, int64_t K, int64_t nstages,
+                                                           int64_t Mp, bool xvec,
+                                                           half8_t* __restrict__ planes) {
+  const int64_t total = nstages * Mp * 16;
+  for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
+       o += (int64_t)gridDim.x * blockDim.x) {
+    const int e = (int)(o & 15);
+    const int64_t r = o >> 4;
+    const int64_t m = r % Mp, st = r / Mp;
+    half8_t hi, lo;
+    stage_entry<BITS>(x, ldx, M, K, (int)(st * 4 + (e >> 2)), e & 3, m, xvec, hi, lo);
+    planes[o] = hi;
+    planes[total + o] = lo;
+  }
+}
+
 template <int BITS, int MTW, int NTW, int WN>
 __global__ __launch_bounds__(64 * WN) void gemm_kernel(
-    const half8_t* __restrict__ xa_hi, const half8_t* __restrict__ xa_lo, int64_t mrows,
+    const half8_t* __restrict__ planes, int64_t Mp, int64_t M,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
-    int64_t ng, int64_t nstages, const float* __restrict__ bias, float* __restrict__ y,
-    int64_t ldy, int64_t M, int64_t N) {
+    int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n,
+    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
+    float* __restrict__ part) {
   constexpr int BM = 16 * MTW;
-  constexpr int ENTRIES = 16 * BM;  // 4 k-steps x 4 quads x BM rows per stage
-  constexpr int RAWN = BITS == 4 ? 1 : 2;
-  __shared__ half8_t l_hi[ENTRIES];
-  __shared__ half8_t l_lo[ENTRIES];
+  constexpr int NTHR = 64 * WN;
+  constexpr int PLANE = BM * 16;           // LDS entries per plane
+  constexpr int CPT = 2 * PLANE / NTHR;    // operand entries each thread copies per stage
+  constexpr int RAWN = BITS == 4 ? 1 : 2;  // 16-byte weight loads per n-tile per stage
+  static_assert(CPT * NTHR == 2 * PLANE, "operand copy must divide evenly");
+  __shared__ half8_t lds[2][2 * PLANE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qd = lane >> 4, c = lane & 15;
-  const int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int64_t n0 = ((int64_t)blockIdx.x * WN + wave) * (16 * NTW);
+
+  // Tile order: consecutive blocks land on different XCDs, so give each XCD a
+  // contiguous range of tiles (m fastest: the m-tiles of one n-tile share
+  // their weight columns through that XCD's L2).
+  const int64_t nblk = gridDim.x, b = blockIdx.x;
+  const int64_t xcd = b % 8, slot = b / 8, q8 = nblk / 8, rem = nblk % 8;
+  const int64_t r = xcd < rem ? xcd * (q8 + 1) + slot : rem * (q8 + 1) + (xcd - rem) * q8 + slot;
+  const int64_t tm = r % tiles_m, rest = r / tiles_m;
+  const int64_t tn = rest % tiles_n, z = rest / tiles_n;
+  const int64_t m0 = tm * BM;
+  const int64_t n0 = (tn * WN + wave) * (16 * NTW);
+  const int64_t sb = z * spz;
+  const int64_t se = sb + spz < nstages ? sb + spz : nstages;
 
   const uint8_t* wrow[NTW];
-  int64_t nrow[NTW];
+  const uint16_t* srow[NTW];
 #pragma unroll
   for (int t = 0; t < NTW; t++) {
     const int64_t n = n0 + t * 16 + c;
-    nrow[t] = n < N ? n : N - 1;
-    wrow[t] = wq + nrow[t] * row_bytes + qd * 16;
+    const int64_t nl = n < N ? n : N - 1;
+    wrow[t] = wq + nl * row_bytes + qd * 16;
+    srow[t] = sc + nl * ng;
   }
+
+  // Operand entry j of this thread: q = tid + j*NTHR -> plane q / PLANE, row
+  // mm, physical slot ph; it holds logical entry ph ^ (mm & 15).
+  int64_t aoff[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; j++) {
+    const int q = tid + j * NTHR;
+    const int p = q / PLANE, rr = q % PLANE;
+    const int mm = rr >> 4, ph = rr & 15;
+    aoff[j] = ((int64_t)p * nstages * Mp + m0 + mm) * 16 + (ph ^ (mm & 15));
+  }
+  u32x4 areg[CPT];
+  auto load_a = [&](int64_t st) {
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+      areg[j] = reinterpret_cast<const u32x4*>(planes)[aoff[j] + st * Mp * 16];
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+      reinterpret_cast<u32x4*>(lds[buf])[tid + j * NTHR] = areg[j];
+  };
+  auto load_w = [&](int64_t st, u32x4 (&dst)[NTW][RAWN], uint16_t (&sdst)[NTW]) {
+#pragma unroll
+    for (int t = 0; t < NTW; t++) {
+#pragma unroll
+      for (int rr = 0; rr < RAWN; rr++)
+        dst[t][rr] = *reinterpret_cast<const u32x4*>(wrow[t] + (st * RAWN + rr) * 64);
+      if constexpr (BITS == 4) sdst[t] = srow[t][st];
+    }
+  };
 
   floatx4 acc[MTW][NTW];
   floatx4 gacc[MTW][NTW];
@@ -388,46 +460,49 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
       gacc[i][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-  for (int64_t st = 0; st < nstages; st++) {
-    u32x4 raw[NTW][RAWN];
-#pragma unroll
-    for (int t = 0; t < NTW; t++)
-#pragma unroll
-      for (int r = 0; r < RAWN; r++)
-        raw[t][r] = *reinterpret_cast<const u32x4*>(wrow[t] + (st * RAWN + r) * 64);
+  // One stage: prefetch stage sn's operands and weights, run the MFMAs of
+  // stage st from LDS buffer buf and registers wc / scur, then copy the
+  // prefetched operands into the other buffer.  Called twice per loop trip
+  // with the weight registers swapped (ping-pong, no register copies), with
+  // no condition inside the trip (a conditional second stage lets the
+  // compiler hoist its loads into the first).
+  auto stage = [&](int64_t st, int buf, const u32x4 (&wc)[NTW][RAWN], const uint16_t (&scur)[NTW],
+                   u32x4 (&wnx)[NTW][RAWN], uint16_t (&snx)[NTW]) {
+    // The last stage reloads itself: unconditional loads keep the memory
+    // counter waits exact.
+    const int64_t sn = st + 1 < se ? st + 1 : st;
+    load_a(sn);
+    load_w(sn, wnx, snx);
+    // Keep the prefetch loads here, ahead of the MFMAs (IR-level and
+    // scheduler fences; neither emits an instruction): left alone, the
+    // compiler sinks them to their uses at the end of the stage, which
+    // serialises load latency and math.
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
-    __syncthreads();
-    for (int e = tid; e < ENTRIES; e += 64 * WN) {
-      const int mm = e % BM, tq = e / BM;  // tq = local T * 4 + qd
-      const int64_t ge = ((st * 4 + (tq >> 2)) * 4 + (tq & 3)) * mrows + m0 + mm;
-      l_hi[e] = xa_hi[ge];
-      l_lo[e] = xa_lo[ge];
-    }
-    __syncthreads();
-
+    const half8_t* la = lds[buf];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      half8_t b[NTW];
+      half8_t bw[NTW];
 #pragma unroll
       for (int t = 0; t < NTW; t++) {
-        if constexpr (BITS == 4) b[t] = int4x8_to_half8(raw[t][0][i]);
-        else b[t] = int8x8_to_half8(raw[t][i >> 1][2 * (i & 1)], raw[t][i >> 1][2 * (i & 1) + 1]);
+        if constexpr (BITS == 4) bw[t] = int4x8_to_half8(wc[t][0][i]);
+        else bw[t] = int8x8_to_half8(wc[t][i >> 1][2 * (i & 1)], wc[t][i >> 1][2 * (i & 1) + 1]);
       }
 #pragma unroll
       for (int mt = 0; mt < MTW; mt++) {
-        const int e = (i * 4 + qd) * BM + mt * 16 + c;
-        const half8_t ah = l_hi[e], al = l_lo[e];
+        const int phys = (mt * 16 + c) * 16 + ((i * 4 + qd) ^ c);
+        const half8_t ah = la[phys], al = la[PLANE + phys];
 #pragma unroll
-        for (int t = 0; t < NTW; t++) {
-          gacc[mt][t] = mfma16x16x32(ah, b[t], gacc[mt][t]);
-          gacc[mt][t] = mfma16x16x32(al, b[t], gacc[mt][t]);
-        }
+        for (int t = 0; t < NTW; t++) gacc[mt][t] = mfma16x16x32(ah, bw[t], gacc[mt][t]);
+#pragma unroll
+        for (int t = 0; t < NTW; t++) gacc[mt][t] = mfma16x16x32(al, bw[t], gacc[mt][t]);
       }
     }
     if constexpr (BITS == 4) {
 #pragma unroll
       for (int t = 0; t < NTW; t++) {
-        const float s = f16_bits_to_f32(sc[nrow[t] * ng + st]);
+        const float s = f16_bits_to_f32(scur[t]);
 #pragma unroll
         for (int mt = 0; mt < MTW; mt++) {
 #pragma unroll
@@ -436,26 +511,84 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
         }
       }
     }
-  }
+    // Copy the prefetched operands only now: the copy waits for their loads,
+    // and that wait must not land among the MFMAs.
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    store_a(buf ^ 1);
+    __syncthreads();
+  };
 
+  u32x4 wa[NTW][RAWN], wb[NTW][RAWN];
+  uint16_t sa[NTW], sbv[NTW];
+  load_a(sb);
+  load_w(sb, wa, sa);
+  store_a(0);
+  __syncthreads();
+  int64_t st = sb;
+  for (; st + 1 < se; st += 2) {
+    stage(st, 0, wa, sa, wb, sbv);
+    stage(st + 1, 1, wb, sbv, wa, sa);
+  }
+  if (st < se) stage(st, 0, wa, sa, wb, sbv);  // odd stage count
+
+  // Lane (qd, c) holds rows 16*mt + 4*qd + i, column 16*t + c of its wave tile.
 #pragma unroll
   for (int t = 0; t < NTW; t++) {
     const int64_t n = n0 + t * 16 + c;
     if (n >= N) continue;
-    float s8 = 1.0f;
-    if constexpr (BITS == 8) s8 = f16_bits_to_f32(sc[n]);
-    const float b = bias ? bias[n] : 0.0f;
+    float s8 = 1.0f, bn = 0.0f;
+    if (part == nullptr) {
+      if constexpr (BITS == 8) s8 = f16_bits_to_f32(sc[n]);
+      if (bias) bn = bias[n];
+    }
 #pragma unroll
     for (int mt = 0; mt < MTW; mt++) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int64_t m = m0 + mt * 16 + 4 * qd + i;
         if (m < M) {
-          const float v = BITS == 4 ? acc[mt][t][i] : gacc[mt][t][i] * s8;
-          y[m * ldy + n] = v + b;
+          const float v = BITS == 4 ? acc[mt][t][i] : gacc[mt][t][i];
+          if (part == nullptr) y[m * ldy + n] = __builtin_fmaf(v, s8, bn);
+          else part[(z * M + m) * N + n] = v;
         }
       }
     }
+  }
+}
+
+// y[m, n] = (sum over z of part[z, m, n]) (* INT8 row scale) + bias, z in
+// order.  VEC: four consecutive n per thread (N % 4 == 0, y rows 16-byte aligned).
+template <int BITS, bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S,
+                                                            int64_t M, int64_t N,
+                                                            const uint16_t* __restrict__ sc,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ y, int64_t ldy) {
+  constexpr int V = VEC ? 4 : 1;
+  const int64_t total = M * N;
+  for (int64_t o = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V; o < total;
+       o += (int64_t)gridDim.x * blockDim.x * V) {
+    const int64_t m = o / N, n = o - m * N;
+    float v[V];
+#pragma unroll
+    for (int u = 0; u < V; u++) v[u] = 0.0f;
+    for (int zz = 0; zz < S; zz++) {
+      if constexpr (VEC) {
+        const float4 p = *reinterpret_cast<const float4*>(part + zz * total + o);
+        v[0] += p.x; v[1] += p.y; v[2] += p.z; v[3] += p.w;
+      } else {
+        v[0] += part[zz * total + o];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < V; u++) {
+      float s8 = 1.0f;
+      if constexpr (BITS == 8) s8 = f16_bits_to_f32(sc[n + u]);
+      v[u] = __builtin_fmaf(v[u], s8, bias ? bias[n + u] : 0.0f);
+    }
+    if constexpr (VEC) *reinterpret_cast<float4*>(y + m * ldy + n) = float4{v[0], v[1], v[2], v[3]};
+    else y[m * ldy + n] = v[0];
   }
 }
 
@@ -509,9 +642,10 @@ constexpr int kSkinnyHLMaxM = 8;             // hi/lo in separate MFMA rows up t
 constexpr int kSkinnyMaxWaves = 16;
 constexpr int64_t kSkinnyTargetWaves = 3072; // ~12 waves per CU across 256 CUs
 constexpr int64_t kSkinnyLdsA = 64 * 1024;   // activation bytes staged in LDS by the workgroup
-constexpr int kGemmMTW = 4, kGemmNTW = 4, kGemmWN = 4;
-constexpr int64_t kGemmBM = 16 * kGemmMTW;
+constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
+constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU
+constexpr int64_t kGemmMinStages = 4;       // stages per K split, at least
 
 enum class Path { Skinny, Gemm, Generic };
 
@@ -525,7 +659,13 @@ struct Plan {
   bool svec = false;    // skinny INT4: vector loads of KS consecutive group scales
   int64_t nunits = 0;   // INT4 groups / INT8 windows per row
   int64_t nT = 0;       // k-steps
-  int64_t mrows = 0;    // staged activation rows (gemm)
+  int mtw = 0;          // gemm: 16-row m-tiles per wave (BM = 16 * mtw)
+  int64_t tiles_m = 0;  // gemm: workgroup tiles along M
+  int64_t tiles_n = 0;  // gemm: workgroup tiles along N
+  int64_t nstages = 0;  // gemm: 128-column K stages
+  int64_t spz = 0;      // gemm: stages per K split
+  int64_t splits = 1;   // gemm: K splits (partials + ordered reduction when > 1)
+  int64_t mpad = 0;     // gemm: operand-plane rows (M rounded up to the row tile)
   int64_t pitch = 0;    // skinny: entries per (quad, A-row) in the lane-major layout
   size_t ws = 0;        // workspace bytes
 };
@@ -569,9 +709,21 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   const int64_t keff = p.nT * 32;
   if (keff % 128 != 0) { p.path = Path::Generic; return p; }
   p.path = Path::Gemm;
-  p.mrows = (m + kGemmBM - 1) / kGemmBM * kGemmBM;
-  p.ws = (size_t)(4 * keff * p.mrows);
-  (void)n;
+  p.mtw = m <= 32 ? 2 : 4;
+  p.tiles_m = (m + 16 * p.mtw - 1) / (16 * p.mtw);
+  p.tiles_n = (n + kGemmBN - 1) / kGemmBN;
+  p.nstages = keff / 128;
+  // Split K only as far as needed to give every CU two workgroups.
+  const int64_t tiles = p.tiles_m * p.tiles_n;
+  int64_t s = 1;
+  if (tiles < kGemmTargetBlocks)
+    s = std::max<int64_t>(1, std::min(kGemmTargetBlocks / tiles, p.nstages / kGemmMinStages));
+  p.spz = (p.nstages + s - 1) / s;
+  p.splits = (p.nstages + p.spz - 1) / p.spz;
+  p.mpad = p.tiles_m * 16 * p.mtw;
+  // Operand planes (2 x 16 bytes per entry), then split-K partials.
+  p.ws = (size_t)(2 * 16 * p.nstages * p.mpad * 16) +
+         (p.splits > 1 ? (size_t)(4 * p.splits * m * n) : 0);
   return p;
 }
 
@@ -639,19 +791,36 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }
 
+template <int BITS, int MTW>
+void launch_gemm_t(const Plan& p, const half8_t* planes, int64_t m, const uint8_t* wq,
+                   const uint16_t* sc, int64_t row_bytes, int64_t ng, const float* bias, float* y,
+                   int64_t ldy, int64_t n, float* part, hipStream_t st) {
+  const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
+  gemm_kernel<BITS, MTW, kGemmNTW, kGemmWN><<<blocks, 64 * kGemmWN, 0, st>>>(
+      planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m, (int)p.tiles_n,
+      bias, y, ldy, n, part);
+}
+
 template <int BITS>
 int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k,
                 const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                 const float* bias, float* y, int64_t ldy, int64_t n, void* ws, hipStream_t st) {
-  half8_t* h = static_cast<half8_t*>(ws);
-  half8_t* l = h + p.nT * 4 * p.mrows;
-  const int64_t entries = p.nT * 4 * p.mrows;
-  unsigned sgrid = (unsigned)std::min<int64_t>((entries + 255) / 256, 8192);
-  stage_gemm_kernel<BITS><<<sgrid, 256, 0, st>>>(x, ldx, m, k, p.nT, p.mrows,
-                                                 x_vectorizable(x, ldx, k), h, l);
-  const dim3 grid((unsigned)((n + kGemmBN - 1) / kGemmBN), (unsigned)(p.mrows / kGemmBM));
-  gemm_kernel<BITS, kGemmMTW, kGemmNTW, kGemmWN><<<grid, 64 * kGemmWN, 0, st>>>(
-      h, l, p.mrows, wq, sc, row_bytes, ng, p.nT / 4, bias, y, ldy, m, n);
+  half8_t* planes = static_cast<half8_t*>(ws);
+  const int64_t entries = p.nstages * p.mpad * 16;
+  const unsigned sg = (unsigned)std::min<int64_t>((entries + 255) / 256, 8192);
+  stage_planes_kernel<BITS><<<sg, 256, 0, st>>>(x, ldx, m, k, p.nstages, p.mpad,
+                                                x_vectorizable(x, ldx, k), planes);
+  float* part = p.splits > 1 ? reinterpret_cast<float*>(planes + 2 * entries) : nullptr;
+  if (p.mtw == 2) launch_gemm_t<BITS, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+  else launch_gemm_t<BITS, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+  if (part) {
+    const bool vec = n % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+                     (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
+    const int64_t items = vec ? m * n / 4 : m * n;
+    const unsigned rg = (unsigned)std::min<int64_t>((items + 255) / 256, 8192);
+    if (vec) splitk_reduce_kernel<BITS, true><<<rg, 256, 0, st>>>(part, (int)p.splits, m, n, sc, bias, y, ldy);
+    else splitk_reduce_kernel<BITS, false><<<rg, 256, 0, st>>>(part, (int)p.splits, m, n, sc, bias, y, ldy);
+  }
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (gemm)" : "kq_linear_int8 (gemm)");
 }
 

@@ -91,6 +91,14 @@ def test_gemm_paths(gpu, scheme, m):
     _run(gpu, m, 250, 640, scheme, seed=m + 9, bias=False)
 
 
+@pytest.mark.parametrize("m", [24, 70])
+def test_gemm_padded_k(gpu, m):
+    # INT4 K = 904 pads to 1024: the last stage holds 8-column chunks past K.
+    _run(gpu, m, 48, 904, "int4", seed=m + 3)
+    # Long K, few tiles: many K splits reduced in order.
+    _run(gpu, m, 40, 8192, "int8", seed=m + 4)
+
+
 @pytest.mark.parametrize("m,n,k,g,scheme", [(16, 512, 512, 32, "int4"), (3, 512, 512, 256, "int4"),
                                             (40, 96, 500, 128, "int4"), (4, 70, 100, 128, "int8"),
                                             (33, 70, 100, 64, "int4"), (2, 16, 1, 128, "int4"),
