@@ -14,6 +14,8 @@ Also reported (same JSON line):
   * skinny M = 8 / 32 / 64 sweeps (continuous-batching decode);
   * INT4 prefill-chunk GEMM TFLOP/s (X [512 x 4096] through gate/up
     [14336 x 4096], then [512 x 14336] through down);
+  * lm_head [128256 x 4096] INT8 / INT4 at M = 1 and 32, alone and followed by
+    the greedy argmax;
   * ``roofline``: the dominant kernel (gate/up projection dequant-GEMV) vs the
     8 TB/s HBM peak;
   * ``cpu_baseline``: the oracle's restatement of the reference forward
@@ -207,6 +209,60 @@ def prefill_tflops(dev, steps, warmup, eager):
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gflop": flops / 1e9}
 
 
+def graph_or_eager(run, eager):
+    if eager:
+        return run
+    run()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    return graph.replay
+
+
+def lm_head(dev, steps, warmup, eager):
+    """Vocab projection [128256 x 4096] (INT8 and INT4 G=128) at M = 1 and 32,
+    then the greedy argmax over each row's logits."""
+    vocab, hidden = 128256, 4096
+    lib = _lib.load()
+    g = torch.Generator(device=dev).manual_seed(11)
+    w = torch.randn(vocab, hidden, device=dev, generator=g) * 0.02
+    out = {}
+    for scheme in ("int8", "int4"):
+        qw = quantize_int8_per_channel(w) if scheme == "int8" else quantize_int4_per_group(w, 128)
+        p = Proj(qw, vocab, hidden, scheme)
+        for m in (1, 32):
+            x = torch.randn(m, hidden, device=dev)
+            y = torch.empty(m, vocab, device=dev)
+            wsb = lib.kq_linear_workspace_bytes(8 if scheme == "int8" else 4, m, vocab, hidden, 128)
+            ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+            tok = torch.empty(m, dtype=torch.int64, device=dev)
+
+            def gemv():
+                p.launch(x, y, ws.data_ptr() if wsb else None, wsb,
+                         torch.cuda.current_stream().cuda_stream)
+
+            def gemv_argmax():
+                gemv()
+                torch.argmax(y, dim=-1, out=tok)
+
+            ms = time_steps(graph_or_eager(gemv, eager), steps, warmup)
+            ms_tok = time_steps(graph_or_eager(gemv_argmax, eager), steps, warmup)
+            nbytes = algorithmic_bytes(m, vocab, hidden, scheme)
+            out[f"{scheme}_m{m}"] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                     "us_gemv": round(ms * 1e3, 2),
+                                     "us_gemv_argmax": round(ms_tok * 1e3, 2),
+                                     "bytes": nbytes}
+        del qw, p
+    del w
+    torch.cuda.synchronize()
+    return out
+
+
 def cpu_baseline(layer, budget_s=20.0):
     """The oracle's restatement of QuantizedLinear.forward (materialise the fp32
     weight, then fp32 BLAS), on this host's cores, over one layer at M = 1."""
@@ -309,6 +365,7 @@ def main():
         breakdown["int4_prefill_m512_mlp"] = {"tflops": round(pf["tflops"], 1), "ms": round(pf["ms"], 3),
                                               "gflop": round(pf["gflop"], 1),
                                               "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}
+        breakdown["lm_head_128256x4096"] = lm_head(dev, args.steps, args.warmup, args.eager)
         cpu = cpu_baseline(int4[0])
 
     # a plain 1 GiB device copy: the reference point for HBM-traffic counters
