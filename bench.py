@@ -40,7 +40,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from kshipra_amd import _lib  # noqa: E402
-from kshipra_amd.quantization import quantize_int4_per_group, quantize_int8_per_channel  # noqa: E402
+from kshipra_amd.quantization import (concat_quantized, quantize_int4_per_group,  # noqa: E402
+                                      quantize_int8_per_channel)
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE counter passes
@@ -51,6 +52,9 @@ LAYERS = 32
 SHAPES = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096),
           ("o_proj", 4096, 4096), ("gate_proj", 14336, 4096), ("up_proj", 14336, 4096),
           ("down_proj", 4096, 14336)]
+# q/k/v and gate/up row-stacked into one weight each: one launch per group.
+FUSED = [("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up", 28672, 4096),
+         ("down_proj", 4096, 14336)]
 
 
 def algorithmic_bytes(m, n, k, scheme):
@@ -92,6 +96,9 @@ def build_layers(scheme, dev, seed, nlayers=LAYERS):
             qw = quantize_int8_per_channel(w) if scheme == "int8" else quantize_int4_per_group(w, 128)
             del w
             layer[name] = Proj(qw, n, k, scheme)
+        for fname, parts in (("qkv", ("q_proj", "k_proj", "v_proj")), ("gate_up", ("gate_proj", "up_proj"))):
+            fq = concat_quantized([layer[p].qw for p in parts])
+            layer[fname] = Proj(fq, fq.original_shape[0], fq.original_shape[1], scheme)
         layers.append(layer)
     torch.cuda.synchronize()
     return layers
@@ -102,7 +109,7 @@ class Sweep:
 
     def __init__(self, layers, m, dev, names=None):
         self.names = names or [s[0] for s in SHAPES]
-        shapes = {s[0]: s for s in SHAPES}
+        shapes = {s[0]: s for s in SHAPES + FUSED}
         self.calls = []
         lib = _lib.load()
         ws_bytes = 0
@@ -332,6 +339,12 @@ def main():
         per_proj[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2),
                           "bytes_per_launch": r["bytes"] // nl}
     breakdown["int4_m1_per_projection"] = per_proj
+    fz = measure(int4, 1, dev, args.steps, args.warmup, args.eager, names=[f[0] for f in FUSED])
+    breakdown["int4_m1_fused_qkv_gateup"] = {"gbs": round(fz["gbs"], 1), "us_per_step": round(fz["ms"] * 1e3, 1)}
+    for name in ("qkv", "gate_up"):
+        r = measure(int4, 1, dev, args.steps, args.warmup, args.eager, names=[name])
+        per_proj[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2),
+                          "bytes_per_launch": r["bytes"] // nl}
     dom = max(("gate_proj", "up_proj", "down_proj"), key=lambda nm: per_proj[nm]["us_per_launch"])
     dom_bytes = per_proj[dom]["bytes_per_launch"]
     dom_us = per_proj[dom]["us_per_launch"]
@@ -352,6 +365,9 @@ def main():
             r = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[name])
             per8[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2)}
         breakdown["int8_m1_per_projection"] = per8
+        fz8 = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[f[0] for f in FUSED])
+        breakdown["int8_m1_fused_qkv_gateup"] = {"gbs": round(fz8["gbs"], 1),
+                                                 "us_per_step": round(fz8["ms"] * 1e3, 1)}
         for m in (8, 32, 64):
             r = measure(int8, m, dev, max(args.steps // 2, 3), 1, args.eager)
             breakdown[f"int8_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),

@@ -13,7 +13,8 @@ decoder that runs every projection through ``QuantizedLinear`` on the GPU.
   length), then M = 1 decode steps, first-index argmax.  The seven projections
   of each layer are ``QuantizedLinear`` modules (the hot path); RMSNorm, RoPE,
   attention over a contiguous KV cache and the fp32 lm_head are plain torch
-  ops on the same device and stream.
+  ops on the same device and stream.  With ``fuse=True`` q/k/v and gate/up run
+  as one ``FusedQuantizedLinear`` launch each (same weights, row-stacked).
 
 Weight dict keys (HF naming): ``embed_tokens.weight``, ``norm.weight``,
 ``lm_head.weight``, ``layers.{i}.{q,k,v,o,gate,up,down}_proj.weight``,
@@ -31,7 +32,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .quantization import QuantizedLinear
+from .quantization import FusedQuantizedLinear, QuantizedLinear
 
 PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
@@ -90,7 +91,8 @@ class DecoderLM:
     """Greedy decoder whose projections are ``QuantizedLinear`` (INT8 / INT4)."""
 
     def __init__(self, cfg: DecoderConfig, weights: Dict[str, torch.Tensor], scheme: str,
-                 device: torch.device, group_size: int = 128, max_seq: int = 256) -> None:
+                 device: torch.device, group_size: int = 128, max_seq: int = 256,
+                 fuse: bool = False) -> None:
         self.cfg = cfg
         self.device = device
         dev = lambda t: torch.as_tensor(t).to(device=device, dtype=torch.float32)
@@ -113,6 +115,9 @@ class DecoderLM:
                         lin.bias.copy_(dev(weights[bias_key]))
                 layer[p] = QuantizedLinear(lin, scheme=scheme, group_size=group_size)
                 del lin
+            if fuse:
+                layer["qkv"] = FusedQuantizedLinear([layer.pop(p) for p in ("q_proj", "k_proj", "v_proj")])
+                layer["gate_up"] = FusedQuantizedLinear([layer.pop(p) for p in ("gate_proj", "up_proj")])
             self.layers.append(layer)
         exps = torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim
         self.inv_freq = (1.0 / (cfg.rope_theta ** exps)).to(device)
@@ -147,9 +152,13 @@ class DecoderLM:
         for li, layer in enumerate(self.layers):
             res = h
             x = _rms_norm(h, layer["in_norm"], c.rms_norm_eps)
-            q = layer["q_proj"](x).view(L, c.num_heads, c.head_dim).transpose(0, 1)
-            k = layer["k_proj"](x).view(L, c.num_kv_heads, c.head_dim).transpose(0, 1)
-            v = layer["v_proj"](x).view(L, c.num_kv_heads, c.head_dim).transpose(0, 1)
+            if "qkv" in layer:
+                q, k, v = layer["qkv"](x)
+            else:
+                q, k, v = layer["q_proj"](x), layer["k_proj"](x), layer["v_proj"](x)
+            q = q.reshape(L, c.num_heads, c.head_dim).transpose(0, 1)
+            k = k.reshape(L, c.num_kv_heads, c.head_dim).transpose(0, 1)
+            v = v.reshape(L, c.num_kv_heads, c.head_dim).transpose(0, 1)
             q = q * cos[None] + _rotate_half(q) * sin[None]
             k = k * cos[None] + _rotate_half(k) * sin[None]
             self.k_cache[li, :, self.pos:S] = k
@@ -163,7 +172,11 @@ class DecoderLM:
             h = res + layer["o_proj"](a.contiguous())
             res = h
             x = _rms_norm(h, layer["post_norm"], c.rms_norm_eps)
-            act = F.silu(layer["gate_proj"](x)) * layer["up_proj"](x)
+            if "gate_up" in layer:
+                gate, up = layer["gate_up"](x)
+            else:
+                gate, up = layer["gate_proj"](x), layer["up_proj"](x)
+            act = F.silu(gate) * up
             h = res + layer["down_proj"](act)
         self.pos = S
         h = _rms_norm(h, self.norm, c.rms_norm_eps)

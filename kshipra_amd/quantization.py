@@ -56,6 +56,8 @@ __all__ = [
     "quantize_int8_per_channel",
     "quantize_int4_per_group",
     "QuantizedLinear",
+    "concat_quantized",
+    "FusedQuantizedLinear",
 ]
 
 
@@ -357,4 +359,76 @@ class QuantizedLinear(nn.Module):
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"scheme={self.scheme}, storage_bytes={self.weight.storage_bytes()}")
+
+
+# ---------------------------------------------------------------------- #
+# Fused projections of one input (q/k/v, gate/up)
+# ---------------------------------------------------------------------- #
+
+
+def concat_quantized(parts) -> QuantizedWeight:
+    """Row-stack quantized weights that share ``in_features`` and scheme.
+
+    Every row (INT8) or row x group (INT4) is quantized on its own
+    (engine/quantization.py:206-208, :293-295), so stacking the payloads and
+    scales equals quantizing the row-stacked fp32 weight -- bit for bit.  One
+    dequant-GEMV over the stacked weight then replaces one launch per part
+    (the adjacent q/k/v calls of engine/model.py:115-117, gate/up of the MLP).
+    """
+    parts = list(parts)
+    if not parts:
+        raise QuantizationError("nothing to concatenate")
+    first = parts[0]
+    for p in parts[1:]:
+        if (p.scheme != first.scheme or p.original_shape[1] != first.original_shape[1]
+                or p.group_size != first.group_size
+                or p.in_features_padded != first.in_features_padded):
+            raise QuantizationError("parts differ in scheme, in_features or group size")
+        if p.payload.device != first.payload.device:
+            raise QuantizationError("parts live on different devices")
+    out = sum(p.original_shape[0] for p in parts)
+    return QuantizedWeight(
+        payload=torch.cat([p.payload for p in parts], dim=0),
+        scales=torch.cat([p.scales for p in parts], dim=0),
+        scheme=first.scheme,
+        original_shape=(out, first.original_shape[1]),
+        group_size=first.group_size,
+        in_features_padded=first.in_features_padded,
+    )
+
+
+class FusedQuantizedLinear(nn.Module):
+    """Several ``QuantizedLinear`` of the same input run as one launch.
+
+    ``forward(x)`` returns one output per part, as views of the single
+    ``[..., sum(out_features)]`` result (same values the parts would give,
+    up to fp32 summation order).  Parts without a bias contribute zeros to the
+    stacked bias when any part has one.
+    """
+
+    def __init__(self, parts) -> None:
+        super().__init__()
+        parts = list(parts)
+        for p in parts:
+            if not isinstance(p, QuantizedLinear):
+                raise QuantizationError(f"expected QuantizedLinear, got {type(p).__name__}")
+        self.in_features = parts[0].in_features
+        self.splits = [p.out_features for p in parts]
+        self.out_features = sum(self.splits)
+        self.scheme = parts[0].scheme
+        self.weight = concat_quantized([p.weight for p in parts])
+        if any(p.bias is not None for p in parts):
+            dev = self.weight.payload.device
+            self.register_buffer("bias", torch.cat([
+                p.bias.detach().to(torch.float32) if p.bias is not None
+                else torch.zeros(p.out_features, dtype=torch.float32, device=dev) for p in parts]))
+        else:
+            self.bias = None
+
+    def forward(self, x: torch.Tensor):
+        return quantized_linear(x, self.weight, self.bias).split(self.splits, dim=-1)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.splits}, "
                 f"scheme={self.scheme}, storage_bytes={self.weight.storage_bytes()}")

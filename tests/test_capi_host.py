@@ -169,3 +169,45 @@ def test_header_cites_reference_for_every_compute_entry_point():
                  "kq_linear_int8", "kq_linear_int4", "kq_check_finite"):
         block = text[:text.index(name + "(")].rsplit("/*", 1)[-1]
         assert "engine/quantization.py" in block, name
+
+
+def _oracle_qw(w, scheme):
+    import numpy as np
+    from oracle import quant
+    if scheme == "int8":
+        p, s = quant.c_quantize_int8(w)
+        return QuantizedWeight(torch.from_numpy(p), torch.from_numpy(s), "int8_per_channel", w.shape)
+    p, s, kp = quant.c_quantize_int4(w, 128)
+    return QuantizedWeight(torch.from_numpy(np.ascontiguousarray(p)), torch.from_numpy(s),
+                           "int4_per_group", w.shape, 128, kp)
+
+
+@pytest.mark.parametrize("scheme", ["int8", "int4"])
+def test_row_stacking_equals_quantizing_the_stacked_weight(scheme):
+    """concat_quantized (the fused q/k/v and gate/up weight) is bit-identical to
+    quantizing the row-stacked fp32 weight, padding columns included."""
+    import numpy as np
+    from cases import gaussian
+    from kshipra_amd.quantization import concat_quantized
+    parts = [gaussian((n, 300), seed=70 + i) for i, n in enumerate((64, 16, 16))]
+    fused = concat_quantized([_oracle_qw(w, scheme) for w in parts])
+    whole = _oracle_qw(np.concatenate(parts, axis=0), scheme)
+    assert fused.original_shape == whole.original_shape == (96, 300)
+    assert torch.equal(fused.payload, whole.payload)
+    assert torch.equal(fused.scales.view(torch.int16), whole.scales.view(torch.int16))
+    assert fused.storage_bytes() == whole.storage_bytes()
+
+
+def test_concat_rejects_mismatched_parts():
+    import numpy as np
+    from cases import gaussian
+    from kshipra_amd.quantization import concat_quantized
+    a = _oracle_qw(gaussian((16, 256), seed=1), "int4")
+    b = _oracle_qw(gaussian((16, 384), seed=2), "int4")
+    c = _oracle_qw(gaussian((16, 256), seed=3), "int8")
+    for bad in ([a, b], [a, c], []):
+        with pytest.raises(QuantizationError):
+            concat_quantized(bad)
+    with pytest.raises(QuantizationError):
+        from kshipra_amd.quantization import FusedQuantizedLinear
+        FusedQuantizedLinear([nn.Linear(4, 4)])

@@ -21,12 +21,12 @@ from oracle import decoder as odec
 pytestmark = pytest.mark.gpu
 
 
-def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed):
+def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed, fuse=False):
     w = decoder_weights(cfg_dict, seed=seed)
     ocfg = odec.DecoderConfig(**cfg_dict)
     gcfg = DecoderConfig(**cfg_dict)
     gpu_lm = DecoderLM(gcfg, {k: torch.from_numpy(v) for k, v in w.items()}, scheme, gpu,
-                       max_seq=len(prompt) + new_tokens + 1)
+                       max_seq=len(prompt) + new_tokens + 1, fuse=fuse)
     toks_g, logits_g = gpu_lm.generate(prompt, new_tokens)
     oracle_lm = odec.OracleDecoder(ocfg, w, scheme)
     toks_o, logits_o = oracle_lm.generate(prompt, new_tokens)
@@ -36,7 +36,7 @@ def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed):
         worst = max(worst, float(np.abs(lg - lo).max() / np.abs(lo).max()))
         top2 = np.sort(lo)[-2:]
         min_gap = min(min_gap, float(top2[1] - top2[0]))
-    print(f"[{scheme} L={cfg_dict['num_layers']} prompt={len(prompt)}] tokens {toks_g} "
+    print(f"[{scheme} L={cfg_dict['num_layers']} prompt={len(prompt)} fuse={fuse}] tokens {toks_g} "
           f"logit rel dev {worst:.3e} min top-2 gap {min_gap:.3e}", flush=True)
     assert toks_g == toks_o
     assert worst < 1e-3
@@ -47,6 +47,12 @@ def test_qwen05b_shaped_greedy_tokens(gpu, scheme):
     """Random-init Qwen2.5-0.5B-shaped decoder (24 layers, 896/4864, 14/2 heads,
     head_dim 64, vocab 151936, q/k/v bias): prefill of 6 tokens then M = 1 decode."""
     _greedy_parity(gpu, QWEN05B, scheme, [1, 42, 100, 201, 7, 999], 8, seed=0)
+
+
+@pytest.mark.parametrize("scheme", ["int4", "int8"])
+def test_qwen05b_shaped_fused_projections(gpu, scheme):
+    """Same model with q/k/v and gate/up each run as one fused launch."""
+    _greedy_parity(gpu, QWEN05B, scheme, [1, 42, 100, 201, 7, 999], 8, seed=0, fuse=True)
 
 
 @pytest.mark.parametrize("scheme", ["int4", "int8"])

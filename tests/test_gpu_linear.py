@@ -22,8 +22,9 @@ import torch
 import torch.nn as nn
 
 from cases import LLAMA3_8B_SHAPES, gaussian, with_outliers
-from kshipra_amd.quantization import (QuantizedLinear, quantize_int4_per_group,
-                                      quantize_int8_per_channel, quantized_linear)
+from kshipra_amd.quantization import (FusedQuantizedLinear, QuantizedLinear,
+                                      quantize_int4_per_group, quantize_int8_per_channel,
+                                      quantized_linear)
 from oracle import quant
 
 pytestmark = pytest.mark.gpu
@@ -230,3 +231,31 @@ def test_linear_without_bias_and_repr(gpu):
     with torch.no_grad():
         assert _rel_l2(lin(x), q(x)) < 2e-2
     assert "scheme=int8" in repr(q) and "storage_bytes=" in repr(q)
+
+
+@pytest.mark.parametrize("scheme", ["int8", "int4"])
+@pytest.mark.parametrize("m", [1, 5, 24, 100])
+def test_fused_projections_match_parts(gpu, scheme, m):
+    """q/k/v-like parts (one without bias) fused into one launch: every part's
+    output against the float64 reference and against its own launch."""
+    k = 896
+    shapes = [(896, k, True), (128, k, False), (128, k, True)]
+    lins = []
+    for i, (n, kk, has_b) in enumerate(shapes):
+        lin = nn.Linear(kk, n, bias=has_b, device=gpu)
+        with torch.no_grad():
+            lin.weight.copy_(torch.from_numpy(gaussian((n, kk), seed=40 + i)))
+            if has_b:
+                lin.bias.copy_(torch.from_numpy(gaussian((n,), seed=50 + i)))
+        lins.append((lin, QuantizedLinear(lin, scheme=scheme)))
+    fused = FusedQuantizedLinear([q for _, q in lins])
+    x = torch.from_numpy(gaussian((m, k), seed=60 + m, std=1.0)).to(gpu)
+    outs = fused(x)
+    assert [o.shape for o in outs] == [(m, n) for n, _, _ in shapes]
+    for (lin, q), o in zip(lins, outs):
+        w = lin.weight.detach().cpu().numpy()
+        b = lin.bias.detach().cpu().numpy() if lin.bias is not None else None
+        y64, mag = _reference(x.cpu().numpy(), w, scheme, 128, b)
+        _compare(o, y64, mag, f"fused part {scheme} m={m} n={w.shape[0]}")
+        sep = q(x)
+        assert torch.allclose(o, sep, rtol=1e-5, atol=1e-5)
