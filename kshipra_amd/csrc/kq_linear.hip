@@ -175,23 +175,24 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
   // the staging are issued first: waiting for them does not wait for the
   // weights.  Then the first chunk of packed weights (and, for INT4, its group
   // scales) goes in flight, then the staging converts while HBM answers.
-  // Staging work split without integer division: thread (wave, lane) owns
-  // k-steps T = wave * 64 + lane + j * 64 * W and stages all 4 * M rows of
-  // each.  The first of them (rows m = 0 of the 4 quads; all of M = 1) is
-  // loaded before the weights.
-  const int t0 = wave * 64 + lane;
-  const int tstride = nwaves * 64;
-  float4 xa4[4], xb4[4];
-  bool pre_ok = false;
+  // Each wave stages only the k-steps of its own units, [ub, ue) * TPU, so a
+  // wave-level sync replaces a workgroup barrier.  Lane l owns entries
+  // e = l + 64 j (k-step ub * TPU + e / 4, quad e % 4) with all M rows; the
+  // first PRE of them (row 0; one batch of KS units' worth) are loaded before
+  // the weights.
+  constexpr int PRE = KS * TPU / 16 < 1 ? 1 : (KS * TPU / 16 > 4 ? 4 : KS * TPU / 16);
+  const int tb = (int)(ub * TPU), te = (int)(ue * TPU);
+  float4 xa4[PRE], xb4[PRE];
+  bool pre_ok[PRE];
   if constexpr (A_LDS) {
-    // All four quads' 8 columns must lie inside the row (quad 3 ends last).
-    pre_ok = xvec && t0 < nT && kstep_col0<BITS>(t0, 3) + 8 <= K;
-    const int tl = pre_ok ? t0 : 0;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; q4++) {
-      const float* src = x + (pre_ok ? kstep_col0<BITS>(tl, q4) : 0);
-      xa4[q4] = reinterpret_cast<const float4*>(src)[0];
-      xb4[q4] = reinterpret_cast<const float4*>(src)[1];
+    for (int j = 0; j < PRE; j++) {
+      const int e = lane + 64 * j;
+      const int T = tb + (e >> 2), q4 = e & 3;
+      pre_ok[j] = xvec && T < te && kstep_col0<BITS>(T, q4) + 8 <= K;
+      const float* src = x + (pre_ok[j] ? kstep_col0<BITS>(T, q4) : 0);
+      xa4[j] = reinterpret_cast<const float4*>(src)[0];
+      xb4[j] = reinterpret_cast<const float4*>(src)[1];
     }
   }
   // Keep these loads ahead of the weight loads (an IR-level ordering fence;
@@ -213,31 +214,36 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
   const half8_t* a = xa;
   if constexpr (A_LDS) {
     half8_t* la = reinterpret_cast<half8_t*>(smem);
-    // Unconditional: a thread without a valid pre-load writes its (unused)
+    // Unconditional: a lane without a valid pre-load writes its (unused)
     // values to the pad column T = nT, which no lane reads.  A branch here
     // would let the compiler sink the pre-loads behind the weight loads.
-    const int tp = pre_ok ? t0 : nT;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; q4++) {
-      const float raw8[8] = {xa4[q4].x, xa4[q4].y, xa4[q4].z, xa4[q4].w,
-                             xb4[q4].x, xb4[q4].y, xb4[q4].z, xb4[q4].w};
+    for (int j = 0; j < PRE; j++) {
+      const int e = lane + 64 * j;
+      const float raw8[8] = {xa4[j].x, xa4[j].y, xa4[j].z, xa4[j].w,
+                             xb4[j].x, xb4[j].y, xb4[j].z, xb4[j].w};
       half8_t hi, lo;
       stage_convert<BITS>(raw8, hi, lo);
-      skinny_store<HL>(la, M, pitch, tp, q4, 0, hi, lo);
+      skinny_store<HL>(la, M, pitch, pre_ok[j] ? tb + (e >> 2) : nT, e & 3, 0, hi, lo);
     }
-    // Everything else (rows m > 0, further k-steps, unaligned x): loaded now,
+    // Everything else (rows m > 0, further entries, unaligned x): loaded now,
     // after the weights are in flight.
-    for (int T = t0; T < nT; T += tstride) {
+    for (int e = lane; e < (te - tb) * 4; e += 64) {
+      const int T = tb + (e >> 2), q4 = e & 3;
+      bool pre = false;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; q4++) {
-        for (int m = (T == t0 && pre_ok) ? 1 : 0; m < M; m++) {
-          half8_t hi, lo;
-          stage_entry<BITS>(x, ldx, M, K, T, q4, m, xvec, hi, lo);
-          skinny_store<HL>(la, M, pitch, T, q4, m, hi, lo);
-        }
+      for (int j = 0; j < PRE; j++) pre = pre || (e == lane + 64 * j && pre_ok[j]);
+      for (int m = pre ? 1 : 0; m < M; m++) {
+        half8_t hi, lo;
+        stage_entry<BITS>(x, ldx, M, K, T, q4, m, xvec, hi, lo);
+        skinny_store<HL>(la, M, pitch, T, q4, m, hi, lo);
       }
     }
-    __syncthreads();
+    // Only this wave reads what it staged: order its LDS writes before its
+    // reads without a workgroup barrier.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     a = la;
   }
 
