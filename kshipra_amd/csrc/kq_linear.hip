@@ -646,7 +646,8 @@ __global__ __launch_bounds__(256) void generic_kernel(const float* __restrict__ 
 constexpr int kSkinnyMaxM = 16;
 constexpr int kSkinnyHLMaxM = 8;             // hi/lo in separate MFMA rows up to M = 8
 constexpr int kSkinnyMaxWaves = 16;
-constexpr int64_t kSkinnyTargetWaves = 3072; // ~12 waves per CU across 256 CUs
+constexpr int64_t kSkinnyMinWaves = 2048;      // 8 waves per CU across 256 CUs
+constexpr int64_t kSkinnyMaxTotalWaves = 12288; // 48 per CU
 constexpr int64_t kSkinnyLdsA = 64 * 1024;   // activation bytes staged in LDS by the workgroup
 constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
@@ -686,18 +687,18 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
     p.path = Path::Skinny;
     p.hl = m <= kSkinnyHLMaxM;
     // Units per wave: a power of two (so every wave's first unit is aligned for
-    // vector scale loads) chosen to bring the total number of waves closest
-    // to ~12 per CU, with at most 16 waves per workgroup.
+    // vector scale loads), at most 16 waves per workgroup.  Measured rule:
+    // 8-unit (8 KB per wave) batches when that still gives >= 2048 waves
+    // (8 per CU); smaller batches for small launches; 16-unit batches only
+    // when 8 would need more than 16 waves per workgroup or > 12288 waves.
     const int64_t ntiles = (n + 15) / 16;
-    int64_t best_pw = 16;
-    double best = 1e30;
-    for (int64_t pw = 2; pw <= 16; pw *= 2) {
-      const int64_t w = (p.nunits + pw - 1) / pw;
-      if (w > kSkinnyMaxWaves) continue;
-      const double r = (double)(ntiles * w) / (double)kSkinnyTargetWaves;
-      const double score = r >= 1.0 ? r : 1.0 / r;
-      if (score < best) { best = score; best_pw = pw; }
+    auto waves_for = [&](int64_t pw) { return ntiles * ((p.nunits + pw - 1) / pw); };
+    int64_t best_pw = 2;
+    for (int64_t pw = 8; pw >= 2; pw /= 2) {
+      if (waves_for(pw) >= kSkinnyMinWaves) { best_pw = pw; break; }
     }
+    if ((p.nunits + 7) / 8 > kSkinnyMaxWaves || waves_for(8) > kSkinnyMaxTotalWaves) best_pw = 16;
+    while ((p.nunits + best_pw - 1) / best_pw > kSkinnyMaxWaves && best_pw < 16) best_pw *= 2;
     p.per_wave = best_pw;
     p.waves = (int)std::min<int64_t>((p.nunits + best_pw - 1) / best_pw, kSkinnyMaxWaves);
     if ((int64_t)p.waves * best_pw < p.nunits)          // K beyond 16 x 16 units: KS-unit chunks
