@@ -233,10 +233,22 @@ __global__ __launch_bounds__(1024) void skinny_kernel(
       bool pre = false;
 #pragma unroll
       for (int j = 0; j < PRE; j++) pre = pre || (e == lane + 64 * j && pre_ok[j]);
-      for (int m = pre ? 1 : 0; m < M; m++) {
-        half8_t hi, lo;
-        stage_entry<BITS>(x, ldx, M, K, T, q4, m, xvec, hi, lo);
-        skinny_store<HL>(la, M, pitch, T, q4, m, hi, lo);
+      // Rows in groups of four: the four rows' loads are issued together
+      // (row index clamped into [0, M), extra rows not stored), so their
+      // latencies overlap instead of adding up.
+      for (int m0 = pre ? 1 : 0; m0 < M; m0 += 4) {
+        float raw8[4][8];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          stage_load<BITS>(x, ldx, M, K, T, q4, m0 + r < M ? m0 + r : M - 1, xvec, raw8[r]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (m0 + r < M) {
+            half8_t hi, lo;
+            stage_convert<BITS>(raw8[r], hi, lo);
+            skinny_store<HL>(la, M, pitch, T, q4, m0 + r, hi, lo);
+          }
+        }
       }
     }
     // Only this wave reads what it staged: order its LDS writes before its
