@@ -151,8 +151,13 @@ __device__ __forceinline__ void load_scales(const uint16_t* __restrict__ srow, i
 // at a time.  The first chunk's weight loads are issued before the
 // activations are staged, so HBM latency overlaps the staging.
 // ---------------------------------------------------------------------------
+// 16-unit batches need more than the 128 VGPRs a 1024-thread workgroup
+// allows: they run at most 8 waves per workgroup (256 VGPRs, no spills).
+template <int KS>
+constexpr int skinny_max_threads() { return KS >= 16 ? 512 : 1024; }
+
 template <int BITS, int KS, bool A_LDS, bool HL, bool SVEC>
-__global__ __launch_bounds__(1024) void skinny_kernel(
+__global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int64_t K, bool xvec,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
@@ -658,6 +663,7 @@ __global__ __launch_bounds__(256) void generic_kernel(const float* __restrict__ 
 constexpr int kSkinnyMaxM = 16;
 constexpr int kSkinnyHLMaxM = 8;             // hi/lo in separate MFMA rows up to M = 8
 constexpr int kSkinnyMaxWaves = 16;
+constexpr int kSkinnyMaxWaves16 = 8;          // with 16-unit batches (skinny_max_threads)
 constexpr int64_t kSkinnyMinWaves = 2048;      // 8 waves per CU across 256 CUs
 constexpr int64_t kSkinnyMaxTotalWaves = 12288; // 48 per CU
 constexpr int64_t kSkinnyLdsA = 64 * 1024;   // activation bytes staged in LDS by the workgroup
@@ -712,8 +718,9 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
     if ((p.nunits + 7) / 8 > kSkinnyMaxWaves || waves_for(8) > kSkinnyMaxTotalWaves) best_pw = 16;
     while ((p.nunits + best_pw - 1) / best_pw > kSkinnyMaxWaves && best_pw < 16) best_pw *= 2;
     p.per_wave = best_pw;
-    p.waves = (int)std::min<int64_t>((p.nunits + best_pw - 1) / best_pw, kSkinnyMaxWaves);
-    if ((int64_t)p.waves * best_pw < p.nunits)          // K beyond 16 x 16 units: KS-unit chunks
+    const int64_t maxw = best_pw >= 16 ? kSkinnyMaxWaves16 : kSkinnyMaxWaves;
+    p.waves = (int)std::min<int64_t>((p.nunits + best_pw - 1) / best_pw, maxw);
+    if ((int64_t)p.waves * best_pw < p.nunits)          // long K: several KS-unit batches
       p.per_wave = (p.nunits + p.waves - 1) / p.waves;
     p.ks = (int)std::min<int64_t>(best_pw, 16);
     p.svec = bits == 4 && p.per_wave % p.ks == 0 && (kp / 128) % p.ks == 0;
