@@ -145,19 +145,23 @@ __device__ __forceinline__ void load_scales(const uint16_t* __restrict__ srow, i
 }
 
 // ---------------------------------------------------------------------------
-// Skinny kernel: M <= 16.  grid.x = ceil(N / 16) column tiles; blockDim =
-// 64 * W; wave w owns units [w * per_wave, (w + 1) * per_wave) of its tile
-// (unit = INT4 group of 128 columns / INT8 window of 64 columns), loaded KS
-// at a time.  The first chunk's weight loads are issued before the
-// activations are staged, so HBM latency overlaps the staging.
+// Skinny kernel: M <= 16.  grid.x = ceil(N / (16 * NT)); a workgroup owns NT
+// adjacent 16-column tiles and blockDim = 64 * W waves split K: wave w owns
+// units [w * per_wave, (w + 1) * per_wave) of every tile (unit = INT4 group
+// of 128 columns / INT8 window of 64 columns), loaded KS at a time.  One
+// activation operand read feeds the NT tiles' MFMAs, and the workgroup's
+// activation staging is shared by 16 * NT columns.  The first chunk's weight
+// loads are issued before the activations are staged, so HBM latency
+// overlaps the staging.
 // ---------------------------------------------------------------------------
-// 16-unit batches need more than the 128 VGPRs a 1024-thread workgroup
-// allows: they run at most 8 waves per workgroup (256 VGPRs, no spills).
-template <int KS>
-constexpr int skinny_max_threads() { return KS >= 16 ? 512 : 1024; }
+// 16 units x tiles per batch need more than the 128 VGPRs a 1024-thread
+// workgroup allows: such kernels run at most 8 waves per workgroup (256 VGPRs,
+// no spills).
+template <int KS, int NT>
+constexpr int skinny_max_threads() { return KS * NT >= 16 ? 512 : 1024; }
 
-template <int BITS, int KS, bool A_LDS, bool HL, bool SVEC>
-__global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
+template <int BITS, int KS, int NT, bool A_LDS, bool HL, bool SVEC>
+__global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int64_t K, bool xvec,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
@@ -170,9 +174,16 @@ __global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
   const int qd = lane >> 4, c = lane & 15;
   const int nT = (int)(nunits * TPU);
 
-  const int64_t n = (int64_t)blockIdx.x * 16 + c;
-  const int64_t nl = n < N ? n : N - 1;
-  const uint8_t* wrow = wq + nl * row_bytes + qd * 16;
+  const int64_t ncol0 = (int64_t)blockIdx.x * 16 * NT;
+  const uint8_t* wrow[NT];
+  const uint16_t* srow[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int64_t n = ncol0 + 16 * t + c;
+    const int64_t nl = n < N ? n : N - 1;
+    wrow[t] = wq + nl * row_bytes + qd * 16;
+    srow[t] = sc + nl * ng;
+  }
   const int64_t ub = (int64_t)wave * per_wave;
   const int64_t ue = ub + per_wave < nunits ? ub + per_wave : nunits;
 
@@ -204,17 +215,20 @@ __global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
   // it emits no instruction and no wait).
   __asm__ volatile("" ::: "memory");
 
-  const uint16_t* srow = sc + nl * ng;
-  u32x4 raw[KS];
-  uint16_t sv[KS];  // raw fp16 bits: converting at load time would force an early wait
+  u32x4 raw[KS][NT];
+  uint16_t sv[NT][KS];  // raw fp16 bits: converting at load time would force an early wait
   // Unconditional (a branch here would make every later wait conservative):
   // units past ue reload unit ue - 1, which is in [0, nunits) for every wave.
 #pragma unroll
   for (int u = 0; u < KS; u++) {
     const int64_t unit = ub + u < ue ? ub + u : ue - 1;
-    raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
+#pragma unroll
+    for (int t = 0; t < NT; t++) raw[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + unit * 64);
   }
-  if constexpr (BITS == 4) load_scales<KS, SVEC>(srow, ub, ue, sv);
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], ub, ue, sv[t]);
+  }
 
   const half8_t* a = xa;
   if constexpr (A_LDS) {
@@ -279,7 +293,9 @@ __global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
     a_lo_lane = a_hi_lane + (int64_t)4 * M * pitch;
   }
 
-  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  floatx4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   half8_t ah[TPU], al[TPU];
 #pragma unroll
   for (int i = 0; i < TPU; i++) { ah[i] = half8_t{}; al[i] = half8_t{}; }
@@ -289,9 +305,13 @@ __global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
 #pragma unroll
       for (int u = 0; u < KS; u++) {
         const int64_t unit = u0 + u < ue ? u0 + u : ue - 1;
-        raw[u] = *reinterpret_cast<const u32x4*>(wrow + unit * 64);
+#pragma unroll
+        for (int t = 0; t < NT; t++) raw[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + unit * 64);
       }
-      if constexpr (BITS == 4) load_scales<KS, SVEC>(srow, u0, ue, sv);
+      if constexpr (BITS == 4) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], u0, ue, sv[t]);
+      }
     }
 #pragma unroll
     for (int u = 0; u < KS; u++) {
@@ -304,23 +324,26 @@ __global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
             if constexpr (!HL) al[i] = a_lo_lane[unit * TPU + i];
           }
         }
-        if constexpr (BITS == 4) {
-          const float s = f16_bits_to_f32(sv[u]);
-          floatx4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const half8_t b = int4x8_to_half8(raw[u][i]);
-            g = mfma16x16x32(ah[i], b, g);
-            if constexpr (!HL) g = mfma16x16x32(al[i], b, g);
-          }
+        for (int t = 0; t < NT; t++) {
+          if constexpr (BITS == 4) {
+            const float s = f16_bits_to_f32(sv[t][u]);
+            floatx4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(s, g[i], acc[i]);
-        } else {
+            for (int i = 0; i < 4; i++) {
+              const half8_t b = int4x8_to_half8(raw[u][t][i]);
+              g = mfma16x16x32(ah[i], b, g);
+              if constexpr (!HL) g = mfma16x16x32(al[i], b, g);
+            }
 #pragma unroll
-          for (int j = 0; j < 2; j++) {
-            const half8_t b = int8x8_to_half8(raw[u][2 * j], raw[u][2 * j + 1]);
-            acc = mfma16x16x32(ah[j], b, acc);
-            if constexpr (!HL) acc = mfma16x16x32(al[j], b, acc);
+            for (int i = 0; i < 4; i++) acc[t][i] = __builtin_fmaf(s, g[i], acc[t][i]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+              const half8_t b = int8x8_to_half8(raw[u][t][2 * j], raw[u][t][2 * j + 1]);
+              acc[t] = mfma16x16x32(ah[j], b, acc[t]);
+              if constexpr (!HL) acc[t] = mfma16x16x32(al[j], b, acc[t]);
+            }
           }
         }
       }
@@ -331,20 +354,24 @@ __global__ __launch_bounds__(skinny_max_threads<KS>()) void skinny_kernel(
   }
 
   // Cross-wave reduction in a fixed order.  Lane (qd, c) holds output-tile
-  // rows 4qd+i, column c (HL: row m is the hi part of x[m], row m + 8 its lo part).
+  // rows 4qd+i, column c of each tile (HL: row m is the hi part of x[m], row
+  // m + 8 its lo part).
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
-  for (int i = 0; i < 4; i++) red[(wave * 16 + 4 * qd + i) * 16 + c] = acc[i];
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[((wave * NT + t) * 16 + 4 * qd + i) * 16 + c] = acc[t][i];
   __syncthreads();
-  for (int o = tid; o < M * 16; o += blockDim.x) {
-    const int m = o >> 4, cc = o & 15;
-    const int64_t nn = (int64_t)blockIdx.x * 16 + cc;
+  for (int o = tid; o < M * 16 * NT; o += blockDim.x) {
+    const int t = o / (M * 16), r = o - t * (M * 16);
+    const int m = r >> 4, cc = r & 15;
+    const int64_t nn = ncol0 + 16 * t + cc;
     if (nn < N) {
       float v = 0.0f;
       for (int w = 0; w < nwaves; w++) {
-        v += red[(w * 16 + m) * 16 + cc];
-        if constexpr (HL) v += red[(w * 16 + m + 8) * 16 + cc];
+        v += red[((w * NT + t) * 16 + m) * 16 + cc];
+        if constexpr (HL) v += red[((w * NT + t) * 16 + m + 8) * 16 + cc];
       }
       if constexpr (BITS == 8) v *= f16_bits_to_f32(sc[nn]);
       if (bias) v += bias[nn];
@@ -666,6 +693,8 @@ constexpr int kSkinnyMaxWaves = 16;
 constexpr int kSkinnyMaxWaves16 = 8;          // with 16-unit batches (skinny_max_threads)
 constexpr int64_t kSkinnyMinWaves = 2048;      // 8 waves per CU across 256 CUs
 constexpr int64_t kSkinnyMaxTotalWaves = 12288; // 48 per CU
+constexpr int kSkinnyNTMinM = 2;                // several 16-column tiles per workgroup from this M
+constexpr int64_t kSkinnyMinGroups = 192;
 constexpr int64_t kSkinnyLdsA = 64 * 1024;   // activation bytes staged in LDS by the workgroup
 constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
@@ -677,6 +706,7 @@ enum class Path { Skinny, Gemm, Generic };
 struct Plan {
   Path path;
   int ks = 0;           // skinny: units per load batch (template)
+  int nt = 1;           // skinny: 16-column tiles per workgroup (template)
   int waves = 0;        // skinny: waves per workgroup
   int64_t per_wave = 0; // skinny: units per wave
   bool a_lds = false;   // skinny: activations staged in LDS by the workgroup
@@ -709,7 +739,15 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
     // 8-unit (8 KB per wave) batches when that still gives >= 2048 waves
     // (8 per CU); smaller batches for small launches; 16-unit batches only
     // when 8 would need more than 16 waves per workgroup or > 12288 waves.
-    const int64_t ntiles = (n + 15) / 16;
+    // Tiles per workgroup: each workgroup stages all of x for its columns, so
+    // wider workgroups cut that traffic (it is M x the weights' own at 16
+    // columns); keep at least 192 workgroups for parallelism.
+    p.nt = 1;
+    if (m >= kSkinnyNTMinM) {
+      const int64_t t16 = (n + 15) / 16;
+      p.nt = t16 / 4 >= kSkinnyMinGroups ? 4 : (t16 / 2 >= kSkinnyMinGroups ? 2 : 1);
+    }
+    const int64_t ntiles = (n + 16 * p.nt - 1) / (16 * p.nt);
     auto waves_for = [&](int64_t pw) { return ntiles * ((p.nunits + pw - 1) / pw); };
     int64_t best_pw = 2;
     for (int64_t pw = 8; pw >= 2; pw /= 2) {
@@ -718,11 +756,12 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
     if ((p.nunits + 7) / 8 > kSkinnyMaxWaves || waves_for(8) > kSkinnyMaxTotalWaves) best_pw = 16;
     while ((p.nunits + best_pw - 1) / best_pw > kSkinnyMaxWaves && best_pw < 16) best_pw *= 2;
     p.per_wave = best_pw;
-    const int64_t maxw = best_pw >= 16 ? kSkinnyMaxWaves16 : kSkinnyMaxWaves;
+    const int64_t maxw = std::min<int64_t>(best_pw, 16 / p.nt) * p.nt >= 16 ? kSkinnyMaxWaves16
+                                                                           : kSkinnyMaxWaves;
     p.waves = (int)std::min<int64_t>((p.nunits + best_pw - 1) / best_pw, maxw);
     if ((int64_t)p.waves * best_pw < p.nunits)          // long K: several KS-unit batches
       p.per_wave = (p.nunits + p.waves - 1) / p.waves;
-    p.ks = (int)std::min<int64_t>(best_pw, 16);
+    p.ks = (int)std::min<int64_t>(best_pw, 16 / p.nt);
     p.svec = bits == 4 && p.per_wave % p.ks == 0 && (kp / 128) % p.ks == 0;
     // An odd pitch puts the four lane quads of an LDS row in different banks;
     // column nT is a pad column (written with unused values, never read).
@@ -762,16 +801,25 @@ void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStrea
                       const float* x, int64_t ldx, int64_t m, int64_t k, bool xvec,
                       const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                       const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n) {
-#define KQ_SKINNY(KS_)                                                                           \
-  skinny_kernel<BITS, KS_, LDS, HL, SVEC><<<grid, block, shm, st>>>(x, ldx, (int)m, k, xvec, wq, sc, \
-                                                              row_bytes, ng, p.nunits,         \
-                                                              p.per_wave, (int)p.pitch, xa,    \
-                                                              bias, y, ldy, n)
-  switch (p.ks) {
-    case 2: KQ_SKINNY(2); break;
-    case 4: KQ_SKINNY(4); break;
-    case 8: KQ_SKINNY(8); break;
-    default: KQ_SKINNY(16); break;
+#define KQ_SKINNY(KS_, NT_)                                                                   \
+  skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC><<<grid, block, shm, st>>>(                     \
+      x, ldx, (int)m, k, xvec, wq, sc, row_bytes, ng, p.nunits, p.per_wave, (int)p.pitch, xa, \
+      bias, y, ldy, n)
+  if (p.nt == 4) {
+    if (p.ks == 2) KQ_SKINNY(2, 4); else KQ_SKINNY(4, 4);
+  } else if (p.nt == 2) {
+    switch (p.ks) {
+      case 2: KQ_SKINNY(2, 2); break;
+      case 4: KQ_SKINNY(4, 2); break;
+      default: KQ_SKINNY(8, 2); break;
+    }
+  } else {
+    switch (p.ks) {
+      case 2: KQ_SKINNY(2, 1); break;
+      case 4: KQ_SKINNY(4, 1); break;
+      case 8: KQ_SKINNY(8, 1); break;
+      default: KQ_SKINNY(16, 1); break;
+    }
   }
 #undef KQ_SKINNY
 }
@@ -792,10 +840,10 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
       stage_skinny_kernel<BITS, false><<<sg, 256, 0, st>>>(x, ldx, (int)m, k, (int)p.nT, p.pitch, xvec, a);
     xa = a;
   }
-  const size_t red = (size_t)p.waves * 256 * sizeof(float);
+  const size_t red = (size_t)p.waves * p.nt * 256 * sizeof(float);
   const size_t abytes = p.a_lds ? (size_t)(128 * p.pitch * m) : 0;
   const size_t shm = std::max(red, abytes);
-  const dim3 grid((unsigned)((n + 15) / 16));
+  const dim3 grid((unsigned)((n + 16 * p.nt - 1) / (16 * p.nt)));
   const dim3 block((unsigned)(64 * p.waves));
   const bool svec = p.svec && reinterpret_cast<uintptr_t>(sc) % (2 * p.ks) == 0;
 #define KQ_SKINNY_SV(LDS_, HL_)                                                                 \
