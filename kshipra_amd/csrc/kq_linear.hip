@@ -607,6 +607,205 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Warp-specialized GEMM (prefill chunks): one producer wave moves each
+// stage's operand block (both planes) and the packed weight columns straight
+// from memory into an LDS ring of D stages with global_load_lds_dwordx4
+// (no registers, no conversion), D - 1 stages ahead of the math; four
+// consumer waves (64 x 64 tiles, BM = 64, BN = 256) only read LDS and run
+// MFMAs.  Synchronisation per stage: the producer waits (explicit vmcnt) for
+// the stage the consumers are about to read, then one s_barrier; the
+// producer's next DMA targets the slot the consumers finished a stage ago.
+// The barrier is a bare s_barrier on purpose: a fenced one would make the
+// producer wait for every DMA in flight, collapsing the ring to one stage.
+//
+// LDS per slot: operand planes (hi, lo) in the layout of gemm_kernel, then
+// the weights: consumer wave w, n-tile t, window r is one 1 KB block whose
+// 16-byte lane slot l holds what MFMA lane l needs (row n0 + 16 t + (l & 15),
+// bytes (l >> 4) * 16 of the stage's window r).
+// ---------------------------------------------------------------------------
+constexpr int kWsConsumers = 4;
+constexpr int kWsThreads = 64 * (kWsConsumers + 1);
+
+__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter limited to n (n < 64).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+template <int BITS, int D>
+__global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
+    const half8_t* __restrict__ planes, int64_t Mp, int64_t M,
+    const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
+    int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n,
+    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
+    float* __restrict__ part) {
+  constexpr int MTW = 4, NTW = 4, BM = 64;
+  constexpr int PLANE = BM * 16;                        // entries per plane
+  constexpr int RAWN = BITS == 4 ? 1 : 2;               // 64-byte windows per stage
+  constexpr int ABLK = 2 * PLANE / 64;                  // 1 KB operand blocks per stage
+  constexpr int WBLK = kWsConsumers * NTW * RAWN;       // 1 KB weight blocks per stage
+  constexpr int SLOT = (ABLK + WBLK) * 64;              // 16-byte entries per slot
+  constexpr int NDMA = ABLK + WBLK;                     // producer DMAs per stage
+  static_assert(NDMA * (D - 2) < 64, "vmcnt range");
+  __shared__ u32x4 ring[D * SLOT];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = wave == kWsConsumers;
+  const int qd = lane >> 4, c = lane & 15;
+
+  const int64_t nblk = gridDim.x, b = blockIdx.x;
+  const int64_t xcd = b % 8, slot = b / 8, q8 = nblk / 8, rem = nblk % 8;
+  const int64_t r = xcd < rem ? xcd * (q8 + 1) + slot : rem * (q8 + 1) + (xcd - rem) * q8 + slot;
+  const int64_t tm = r % tiles_m, rest = r / tiles_m;
+  const int64_t tn = rest % tiles_n, z = rest / tiles_n;
+  const int64_t m0 = tm * BM;
+  const int64_t nb = tn * kWsConsumers * 16 * NTW;      // first column of the workgroup
+  const int64_t sb = z * spz;
+  const int64_t se = sb + spz < nstages ? sb + spz : nstages;
+  const int64_t nst = se - sb;
+
+  // Producer addressing: operand block j -> plane j / (BM/4), rows 4 (j % (BM/4)) + (lane >> 4);
+  // weight block (w, t, rr) -> row nb + 64 w + 16 t + (lane & 15), byte (lane >> 4) * 16.
+  auto issue = [&](int64_t st, int sl) {
+    u32x4* base = ring + sl * SLOT;
+#pragma unroll
+    for (int j = 0; j < ABLK; j++) {
+      const int p = j / (BM / 4), mm = (j % (BM / 4)) * 4 + (lane >> 4), ph = lane & 15;
+      const int64_t e = ((p * nstages + st) * Mp + m0 + mm) * 16 + (ph ^ (mm & 15));
+      dma16(planes + e, base + j * 64);
+    }
+#pragma unroll
+    for (int w = 0; w < kWsConsumers; w++)
+#pragma unroll
+      for (int t = 0; t < NTW; t++) {
+        const int64_t n = nb + 64 * w + 16 * t + (lane & 15);
+        const uint8_t* src = wq + (n < N ? n : N - 1) * row_bytes + (lane >> 4) * 16;
+#pragma unroll
+        for (int rr = 0; rr < RAWN; rr++)
+          dma16(src + (st * RAWN + rr) * 64, base + (ABLK + (w * NTW + t) * RAWN + rr) * 64);
+      }
+  };
+
+  floatx4 acc[MTW][NTW];
+  floatx4 gacc[MTW][NTW];
+#pragma unroll
+  for (int i = 0; i < MTW; i++)
+#pragma unroll
+    for (int t = 0; t < NTW; t++) {
+      acc[i][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      gacc[i][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  const int64_t n0 = nb + 64 * (producer ? 0 : wave);
+  const uint16_t* srow[NTW];
+#pragma unroll
+  for (int t = 0; t < NTW; t++) {
+    const int64_t n = n0 + 16 * t + c;
+    srow[t] = sc + (n < N ? n : N - 1) * ng;
+  }
+
+  // Producer and consumers run separate loops with the same number of
+  // barriers (one per stage), so neither path's registers burden the other.
+  if (producer) {
+#pragma unroll
+    for (int k = 0; k < D - 1; k++) issue(sb + (k < nst ? k : nst - 1), k);
+    for (int64_t s = 0; s < nst; s++) {
+      wait_vmcnt<NDMA * (D - 2)>();               // stage s has landed
+      __builtin_amdgcn_s_barrier();
+      const int64_t k = s + D - 1;                // into the slot read a stage ago
+      issue(sb + (k < nst ? k : nst - 1), (int)(k % D));
+    }
+    return;
+  }
+
+  uint16_t scur[NTW];
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int t = 0; t < NTW; t++) scur[t] = srow[t][sb];
+  }
+  for (int64_t s = 0; s < nst; s++) {
+    wait_lgkmcnt0();                              // this wave's reads of stage s - 1 are done
+    __builtin_amdgcn_s_barrier();
+    uint16_t snx[NTW];
+    if constexpr (BITS == 4) {
+      const int64_t sn = sb + (s + 1 < nst ? s + 1 : s);
+#pragma unroll
+      for (int t = 0; t < NTW; t++) snx[t] = srow[t][sn];
+    }
+    const u32x4* base = ring + (int)(s % D) * SLOT;
+    const half8_t* la = reinterpret_cast<const half8_t*>(base);
+    u32x4 wr[NTW][RAWN];
+#pragma unroll
+    for (int t = 0; t < NTW; t++)
+#pragma unroll
+      for (int rr = 0; rr < RAWN; rr++)
+        wr[t][rr] = base[(ABLK + (wave * NTW + t) * RAWN + rr) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      half8_t bw[NTW];
+#pragma unroll
+      for (int t = 0; t < NTW; t++) {
+        if constexpr (BITS == 4) bw[t] = int4x8_to_half8(wr[t][0][i]);
+        else bw[t] = int8x8_to_half8(wr[t][i >> 1][2 * (i & 1)], wr[t][i >> 1][2 * (i & 1) + 1]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MTW; mt++) {
+        const int phys = (mt * 16 + c) * 16 + ((i * 4 + qd) ^ c);
+        const half8_t ah = la[phys], al = la[PLANE + phys];
+#pragma unroll
+        for (int t = 0; t < NTW; t++) gacc[mt][t] = mfma16x16x32(ah, bw[t], gacc[mt][t]);
+#pragma unroll
+        for (int t = 0; t < NTW; t++) gacc[mt][t] = mfma16x16x32(al, bw[t], gacc[mt][t]);
+      }
+    }
+    if constexpr (BITS == 4) {
+#pragma unroll
+      for (int t = 0; t < NTW; t++) {
+        const float sf = f16_bits_to_f32(scur[t]);
+#pragma unroll
+        for (int mt = 0; mt < MTW; mt++) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[mt][t][i] = __builtin_fmaf(sf, gacc[mt][t][i], acc[mt][t][i]);
+          gacc[mt][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        scur[t] = snx[t];
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < NTW; t++) {
+    const int64_t n = n0 + t * 16 + c;
+    if (n >= N) continue;
+    float s8 = 1.0f, bn = 0.0f;
+    if (part == nullptr) {
+      if constexpr (BITS == 8) s8 = f16_bits_to_f32(sc[n]);
+      if (bias) bn = bias[n];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTW; mt++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int64_t m = m0 + mt * 16 + 4 * qd + i;
+        if (m < M) {
+          const float v = BITS == 4 ? acc[mt][t][i] : gacc[mt][t][i];
+          if (part == nullptr) y[m * ldy + n] = __builtin_fmaf(v, s8, bn);
+          else part[(z * M + m) * N + n] = v;
+        }
+      }
+    }
+  }
+}
+
 // y[m, n] = (sum over z of part[z, m, n]) (* INT8 row scale) + bias, z in
 // order.  VEC: four consecutive n per thread (N % 4 == 0, y rows 16-byte aligned).
 template <int BITS, bool VEC>
@@ -700,6 +899,8 @@ constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
 constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU
 constexpr int64_t kGemmMinStages = 4;       // stages per K split, at least
+constexpr int64_t kGemmWsMinM = 128;        // warp-specialized DMA kernel from this M
+constexpr int64_t kGemmWsTargetBlocks = 256;  // one resident workgroup per CU (LDS ring)
 
 enum class Path { Skinny, Gemm, Generic };
 
@@ -721,6 +922,7 @@ struct Plan {
   int64_t spz = 0;      // gemm: stages per K split
   int64_t splits = 1;   // gemm: K splits (partials + ordered reduction when > 1)
   int64_t mpad = 0;     // gemm: operand-plane rows (M rounded up to the row tile)
+  bool wspec = false;   // gemm: warp-specialized DMA kernel (prefill chunks)
   int64_t pitch = 0;    // skinny: entries per (quad, A-row) in the lane-major layout
   size_t ws = 0;        // workspace bytes
 };
@@ -774,15 +976,17 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   const int64_t keff = p.nT * 32;
   if (keff % 128 != 0) { p.path = Path::Generic; return p; }
   p.path = Path::Gemm;
-  p.mtw = m <= 32 ? 2 : 4;
+  p.wspec = m >= kGemmWsMinM;
+  p.mtw = (m <= 32 && !p.wspec) ? 2 : 4;
   p.tiles_m = (m + 16 * p.mtw - 1) / (16 * p.mtw);
   p.tiles_n = (n + kGemmBN - 1) / kGemmBN;
   p.nstages = keff / 128;
   // Split K only as far as needed to give every CU two workgroups.
   const int64_t tiles = p.tiles_m * p.tiles_n;
+  const int64_t target = p.wspec ? kGemmWsTargetBlocks : kGemmTargetBlocks;
   int64_t s = 1;
-  if (tiles < kGemmTargetBlocks)
-    s = std::max<int64_t>(1, std::min(kGemmTargetBlocks / tiles, p.nstages / kGemmMinStages));
+  if (tiles < target)
+    s = std::max<int64_t>(1, std::min(target / tiles, p.nstages / kGemmMinStages));
   p.spz = (p.nstages + s - 1) / s;
   p.splits = (p.nstages + p.spz - 1) / p.spz;
   p.mpad = p.tiles_m * 16 * p.mtw;
@@ -885,8 +1089,16 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
   stage_planes_kernel<BITS><<<sg, 256, 0, st>>>(x, ldx, m, k, p.nstages, p.mpad,
                                                 x_vectorizable(x, ldx, k), planes);
   float* part = p.splits > 1 ? reinterpret_cast<float*>(planes + 2 * entries) : nullptr;
-  if (p.mtw == 2) launch_gemm_t<BITS, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
-  else launch_gemm_t<BITS, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+  if (p.wspec) {
+    const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
+    gemm_ws_kernel<BITS, BITS == 4 ? 3 : 2><<<blocks, kWsThreads, 0, st>>>(
+        planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m,
+        (int)p.tiles_n, bias, y, ldy, n, part);
+  } else if (p.mtw == 2) {
+    launch_gemm_t<BITS, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+  } else {
+    launch_gemm_t<BITS, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+  }
   if (part) {
     const bool vec = n % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
                      (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0);

@@ -100,6 +100,14 @@ def test_gemm_padded_k(gpu, m):
     _run(gpu, m, 40, 8192, "int8", seed=m + 4)
 
 
+@pytest.mark.parametrize("m,n,k,scheme", [(130, 80, 100, "int4"), (129, 300, 128, "int8"),
+                                          (200, 70, 1280, "int4"), (256, 528, 384, "int8")])
+def test_gemm_prefill_kernel_edges(gpu, m, n, k, scheme):
+    """Prefill-sized M through the producer/consumer kernel: one or few K
+    stages (shorter than the LDS ring), partial row and column tiles, splits."""
+    _run(gpu, m, n, k, scheme, seed=m + n)
+
+
 @pytest.mark.parametrize("m,n,k,g,scheme", [(16, 512, 512, 32, "int4"), (3, 512, 512, 256, "int4"),
                                             (40, 96, 500, 128, "int4"), (4, 70, 100, 128, "int8"),
                                             (33, 70, 100, 64, "int4"), (2, 16, 1, 128, "int4"),
