@@ -697,14 +697,10 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
   };
 
   floatx4 acc[MTW][NTW];
-  floatx4 gacc[MTW][NTW];
 #pragma unroll
   for (int i = 0; i < MTW; i++)
 #pragma unroll
-    for (int t = 0; t < NTW; t++) {
-      acc[i][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-      gacc[i][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    for (int t = 0; t < NTW; t++) acc[i][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   const int64_t n0 = nb + 64 * (producer ? 0 : wave);
   const uint16_t* srow[NTW];
 #pragma unroll
@@ -749,35 +745,45 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
 #pragma unroll
       for (int rr = 0; rr < RAWN; rr++)
         wr[t][rr] = base[(ABLK + (wave * NTW + t) * RAWN + rr) * 64 + lane];
+    // The stage's B operands (4 k-steps x NTW tiles), converted once.
+    half8_t bw[4][NTW];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      half8_t bw[NTW];
+    for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int t = 0; t < NTW; t++) {
-        if constexpr (BITS == 4) bw[t] = int4x8_to_half8(wr[t][0][i]);
-        else bw[t] = int8x8_to_half8(wr[t][i >> 1][2 * (i & 1)], wr[t][i >> 1][2 * (i & 1) + 1]);
+        if constexpr (BITS == 4) bw[i][t] = int4x8_to_half8(wr[t][0][i]);
+        else bw[i][t] = int8x8_to_half8(wr[t][i >> 1][2 * (i & 1)], wr[t][i >> 1][2 * (i & 1) + 1]);
       }
+    float sf[NTW];
+    if constexpr (BITS == 4) {
 #pragma unroll
-      for (int mt = 0; mt < MTW; mt++) {
+      for (int t = 0; t < NTW; t++) { sf[t] = f16_bits_to_f32(scur[t]); scur[t] = snx[t]; }
+    }
+    // One 16-row m-tile at a time through all four k-steps: INT4 applies the
+    // group scale to that m-tile's partial sums while the next m-tile's
+    // MFMAs run, instead of draining every accumulator at the stage's end.
+#pragma unroll
+    for (int mt = 0; mt < MTW; mt++) {
+      floatx4 g[NTW];
+#pragma unroll
+      for (int t = 0; t < NTW; t++) g[t] = BITS == 4 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : acc[mt][t];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
         const int phys = (mt * 16 + c) * 16 + ((i * 4 + qd) ^ c);
         const half8_t ah = la[phys], al = la[PLANE + phys];
 #pragma unroll
-        for (int t = 0; t < NTW; t++) gacc[mt][t] = mfma16x16x32(ah, bw[t], gacc[mt][t]);
+        for (int t = 0; t < NTW; t++) g[t] = mfma16x16x32(ah, bw[i][t], g[t]);
 #pragma unroll
-        for (int t = 0; t < NTW; t++) gacc[mt][t] = mfma16x16x32(al, bw[t], gacc[mt][t]);
+        for (int t = 0; t < NTW; t++) g[t] = mfma16x16x32(al, bw[i][t], g[t]);
       }
-    }
-    if constexpr (BITS == 4) {
 #pragma unroll
       for (int t = 0; t < NTW; t++) {
-        const float sf = f16_bits_to_f32(scur[t]);
+        if constexpr (BITS == 4) {
 #pragma unroll
-        for (int mt = 0; mt < MTW; mt++) {
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[mt][t][i] = __builtin_fmaf(sf, gacc[mt][t][i], acc[mt][t][i]);
-          gacc[mt][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+          for (int i = 0; i < 4; i++) acc[mt][t][i] = __builtin_fmaf(sf[t], g[t][i], acc[mt][t][i]);
+        } else {
+          acc[mt][t] = g[t];
         }
-        scur[t] = snx[t];
       }
     }
   }
@@ -797,7 +803,7 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
       for (int i = 0; i < 4; i++) {
         const int64_t m = m0 + mt * 16 + 4 * qd + i;
         if (m < M) {
-          const float v = BITS == 4 ? acc[mt][t][i] : gacc[mt][t][i];
+          const float v = acc[mt][t][i];
           if (part == nullptr) y[m * ldy + n] = __builtin_fmaf(v, s8, bn);
           else part[(z * M + m) * N + n] = v;
         }
