@@ -905,7 +905,7 @@ constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
 constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU
 constexpr int64_t kGemmMinStages = 4;       // stages per K split, at least
-constexpr int64_t kGemmWsMinM = 128;        // warp-specialized DMA kernel from this M
+constexpr int64_t kGemmWsMinM = 33;         // warp-specialized DMA kernel from this M
 constexpr int64_t kGemmWsTargetBlocks = 256;  // one resident workgroup per CU (LDS ring)
 
 enum class Path { Skinny, Gemm, Generic };
