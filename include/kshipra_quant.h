@@ -100,6 +100,30 @@ int kq_linear_int4(const float* x, int64_t m, int64_t ldx, const uint8_t* payloa
                    const float* bias, float* y, int64_t ldy, int64_t n, int64_t k,
                    void* workspace, size_t workspace_bytes, kq_stream_t stream);
 
+/* Workspace bytes for kq_linear_argmax_int8 / _int4 with these sizes (host
+ * only; scheme 8 or 4). */
+size_t kq_linear_argmax_workspace_bytes(int scheme, int64_t m, int64_t n, int64_t k,
+                                        int64_t group_size);
+
+/* Quantized vocab projection + greedy token (engine/model.py:151 computes the
+ * logits, :187 and :200 take int(logits[0, -1].argmax())): the same sum as
+ * kq_linear_int8, then tokens[r] = first index of the maximum of row r
+ * (a NaN counts as the maximum, as torch.argmax).  logits: [m, n] (ldl) or
+ * NULL to skip writing them; tokens: int64 [m].  m <= 65535, n < 2^31.
+ * workspace: at least kq_linear_argmax_workspace_bytes(8, ...) bytes. */
+int kq_linear_argmax_int8(const float* x, int64_t m, int64_t ldx, const int8_t* payload,
+                          const uint16_t* scales, const float* bias, float* logits,
+                          int64_t ldl, int64_t n, int64_t k, int64_t* tokens, void* workspace,
+                          size_t workspace_bytes, kq_stream_t stream);
+
+/* As kq_linear_argmax_int8 over the INT4 payload (engine/model.py:151,187,200
+ * with the projection of kq_linear_int4). */
+int kq_linear_argmax_int4(const float* x, int64_t m, int64_t ldx, const uint8_t* payload,
+                          const uint16_t* scales, int64_t group_size, int64_t k_padded,
+                          const float* bias, float* logits, int64_t ldl, int64_t n, int64_t k,
+                          int64_t* tokens, void* workspace, size_t workspace_bytes,
+                          kq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -145,6 +145,28 @@ __device__ __forceinline__ void load_scales(const uint16_t* __restrict__ srow, i
 }
 
 // ---------------------------------------------------------------------------
+// Greedy argmax (engine/model.py:187,200: first index of the maximum, as
+// torch.argmax): a NaN counts as larger than every number; among equal
+// values (+0 == -0) the smaller index wins.  Partials are (value bits, index)
+// pairs; index INT32_MAX marks "no column".
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool arg_better(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an || bn) return an && (!bn || ai < bi);
+  return av > bv || (av == bv && ai < bi);
+}
+
+// Reduce a (value, index) pair over the 16 lanes of each 16-lane group.
+__device__ __forceinline__ void arg_reduce16(float& v, int& i) {
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(i, off);
+    if (arg_better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny kernel: M <= 16.  grid.x = ceil(N / (16 * NT)); a workgroup owns NT
 // adjacent 16-column tiles and blockDim = 64 * W waves split K: wave w owns
 // units [w * per_wave, (w + 1) * per_wave) of every tile (unit = INT4 group
@@ -165,7 +187,8 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int64_t K, bool xvec,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
-    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N) {
+    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
+    int2* __restrict__ argp) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int TPU = BITS == 4 ? 4 : 2;  // k-steps per unit
   const int tid = threadIdx.x, lane = tid & 63;
@@ -363,19 +386,29 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 #pragma unroll
     for (int i = 0; i < 4; i++) red[((wave * NT + t) * 16 + 4 * qd + i) * 16 + c] = acc[t][i];
   __syncthreads();
+  // y may be null (greedy argmax only).  With argp, the 16 lanes of a row's
+  // tile reduce their (logit, column) pairs and lane 0 writes the tile's
+  // partial: argp[m * tiles + tile].
   for (int o = tid; o < M * 16 * NT; o += blockDim.x) {
     const int t = o / (M * 16), r = o - t * (M * 16);
     const int m = r >> 4, cc = r & 15;
     const int64_t nn = ncol0 + 16 * t + cc;
+    float v = -__builtin_inff();
+    int vi = 0x7fffffff;
     if (nn < N) {
-      float v = 0.0f;
+      v = 0.0f;
       for (int w = 0; w < nwaves; w++) {
         v += red[((w * NT + t) * 16 + m) * 16 + cc];
         if constexpr (HL) v += red[((w * NT + t) * 16 + m + 8) * 16 + cc];
       }
       if constexpr (BITS == 8) v *= f16_bits_to_f32(sc[nn]);
       if (bias) v += bias[nn];
-      y[m * ldy + nn] = v;
+      if (y) y[m * ldy + nn] = v;
+      vi = (int)nn;
+    }
+    if (argp) {
+      arg_reduce16(v, vi);
+      if (cc == 0) argp[(int64_t)m * gridDim.x * NT + blockIdx.x * NT + t] = make_int2(__float_as_int(v), vi);
     }
   }
 }
@@ -812,6 +845,65 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
   }
 }
 
+// Row argmax, pass 1 over materialised logits: block (chunk, m) reduces
+// columns [chunk * 4096, +4096) of row m to argp[m * chunks + chunk].
+constexpr int kArgChunk = 4096;
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ y, int64_t ldy,
+                                                             int64_t N, int2* __restrict__ argp) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int64_t m = blockIdx.y, c0 = (int64_t)blockIdx.x * kArgChunk;
+  float v = -__builtin_inff();
+  int vi = 0x7fffffff;
+  for (int64_t c = c0 + threadIdx.x; c < c0 + kArgChunk && c < N; c += 256) {
+    const float a = y[m * ldy + c];
+    if (arg_better(a, (int)c, v, vi)) { v = a; vi = (int)c; }
+  }
+  arg_reduce16(v, vi);
+#pragma unroll
+  for (int off = 16; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(vi, off);
+    if (arg_better(ov, oi, v, vi)) { v = ov; vi = oi; }
+  }
+  if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = vi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++)
+      if (arg_better(sv[w], si[w], v, vi)) { v = sv[w]; vi = si[w]; }
+    argp[m * gridDim.x + blockIdx.x] = make_int2(__float_as_int(v), vi);
+  }
+}
+
+// Row argmax, pass 2: block m reduces the row's `parts` partials to tokens[m].
+__global__ __launch_bounds__(256) void argmax_final_kernel(const int2* __restrict__ argp, int64_t parts,
+                                                           int64_t* __restrict__ tokens) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int64_t m = blockIdx.x;
+  float v = -__builtin_inff();
+  int vi = 0x7fffffff;
+  for (int64_t j = threadIdx.x; j < parts; j += 256) {
+    const int2 q = argp[m * parts + j];
+    const float a = __int_as_float(q.x);
+    if (arg_better(a, q.y, v, vi)) { v = a; vi = q.y; }
+  }
+  arg_reduce16(v, vi);
+#pragma unroll
+  for (int off = 16; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(vi, off);
+    if (arg_better(ov, oi, v, vi)) { v = ov; vi = oi; }
+  }
+  if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = vi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++)
+      if (arg_better(sv[w], si[w], v, vi)) { v = sv[w]; vi = si[w]; }
+    tokens[m] = vi;
+  }
+}
+
 // y[m, n] = (sum over z of part[z, m, n]) (* INT8 row scale) + bias, z in
 // order.  VEC: four consecutive n per thread (N % 4 == 0, y rows 16-byte aligned).
 template <int BITS, bool VEC>
@@ -1010,11 +1102,12 @@ template <int BITS, bool LDS, bool HL, bool SVEC>
 void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStream_t st,
                       const float* x, int64_t ldx, int64_t m, int64_t k, bool xvec,
                       const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
-                      const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n) {
+                      const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n,
+                      int2* argp) {
 #define KQ_SKINNY(KS_, NT_)                                                                   \
   skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC><<<grid, block, shm, st>>>(                     \
       x, ldx, (int)m, k, xvec, wq, sc, row_bytes, ng, p.nunits, p.per_wave, (int)p.pitch, xa, \
-      bias, y, ldy, n)
+      bias, y, ldy, n, argp)
   if (p.nt == 4) {
     if (p.ks == 2) KQ_SKINNY(2, 4); else KQ_SKINNY(4, 4);
   } else if (p.nt == 2) {
@@ -1037,7 +1130,8 @@ void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStrea
 template <int BITS>
 int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k,
                   const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
-                  const float* bias, float* y, int64_t ldy, int64_t n, void* ws, hipStream_t st) {
+                  const float* bias, float* y, int64_t ldy, int64_t n, void* ws, hipStream_t st,
+                  int2* argp = nullptr) {
   const bool xvec = x_vectorizable(x, ldx, k);
   const half8_t* xa = nullptr;
   if (!p.a_lds) {
@@ -1060,9 +1154,10 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   do {                                                                                          \
     if (svec) launch_skinny_ks<BITS, LDS_, HL_, true>(p, grid, block, shm, st, x, ldx, m, k,   \
                                                       xvec, wq, sc, row_bytes, ng, xa, bias, y, \
-                                                      ldy, n);                                  \
+                                                      ldy, n, argp);                            \
     else launch_skinny_ks<BITS, LDS_, HL_, false>(p, grid, block, shm, st, x, ldx, m, k, xvec,  \
-                                                  wq, sc, row_bytes, ng, xa, bias, y, ldy, n);  \
+                                                  wq, sc, row_bytes, ng, xa, bias, y, ldy, n,   \
+                                                  argp);                                        \
   } while (0)
   if (p.a_lds) {
     if (p.hl) KQ_SKINNY_SV(true, true);
@@ -1125,6 +1220,26 @@ int launch_generic(const float* x, int64_t ldx, int64_t m, const uint8_t* wq, co
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (generic)" : "kq_linear_int8 (generic)");
 }
 
+// Workspace of the linear + greedy-argmax entry points: the linear's own
+// workspace, then the per-row partials, then (GEMM / generic paths) a logits
+// buffer used when the caller passes none.
+struct ArgLayout {
+  int64_t parts = 0;
+  size_t part_off = 0, logit_off = 0, total = 0;
+};
+
+inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+ArgLayout arg_layout(const Plan& p, int64_t m, int64_t n) {
+  ArgLayout a;
+  const bool skinny = p.path == Path::Skinny;
+  a.parts = skinny ? (n + 16 * p.nt - 1) / (16 * p.nt) * p.nt : (n + kArgChunk - 1) / kArgChunk;
+  a.part_off = align256(p.ws);
+  a.logit_off = align256(a.part_off + (size_t)(m * a.parts) * sizeof(int2));
+  a.total = a.logit_off + (skinny ? 0 : (size_t)(m * n) * sizeof(float));
+  return a;
+}
+
 int check_linear_args(const float* x, int64_t m, int64_t ldx, const void* wq, const void* sc,
                       float* y, int64_t ldy, int64_t n, int64_t k) {
   KQ_REQUIRE(x != nullptr && wq != nullptr && sc != nullptr && y != nullptr, "null pointer argument");
@@ -1179,4 +1294,79 @@ extern "C" int kq_linear_int4(const float* x, int64_t m, int64_t ldx, const uint
     case Path::Gemm: return launch_gemm<4>(p, x, ldx, m, k, payload, scales, kp / 2, ng, bias, y, ldy, n, ws, st);
     default: return launch_generic<4>(x, ldx, m, payload, scales, kp / 2, g, ng, bias, y, ldy, n, k, st);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Quantized linear + greedy argmax (the lm_head of engine/model.py:151, read
+// by :187,:200): tokens[r] = first index of the maximum of row r's logits.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int BITS>
+int linear_argmax(const Plan& p, const float* x, int64_t m, int64_t ldx, const uint8_t* wq,
+                  const uint16_t* sc, int64_t row_bytes, int64_t g, int64_t ng, const float* bias,
+                  float* logits, int64_t ldl, int64_t n, int64_t k, int64_t* tokens, void* ws,
+                  size_t ws_bytes, hipStream_t st) {
+  const ArgLayout a = arg_layout(p, m, n);
+  if (ws == nullptr || ws_bytes < a.total)
+    return kq_set_error(KQ_ERR_WORKSPACE, "workspace missing or smaller than kq_linear_argmax_workspace_bytes()");
+  char* w = static_cast<char*>(ws);
+  int2* argp = reinterpret_cast<int2*>(w + a.part_off);
+  int s;
+  if (p.path == Path::Skinny) {
+    s = launch_skinny<BITS>(p, x, ldx, m, k, wq, sc, row_bytes, ng, bias, logits, ldl, n, w, st, argp);
+  } else {
+    float* y = logits ? logits : reinterpret_cast<float*>(w + a.logit_off);
+    const int64_t ldy = logits ? ldl : n;
+    if (p.path == Path::Gemm) s = launch_gemm<BITS>(p, x, ldx, m, k, wq, sc, row_bytes, ng, bias, y, ldy, n, w, st);
+    else s = launch_generic<BITS>(x, ldx, m, wq, sc, row_bytes, g, ng, bias, y, ldy, n, k, st);
+    if (s == KQ_OK) argmax_partial_kernel<<<dim3((unsigned)a.parts, (unsigned)m), 256, 0, st>>>(y, ldy, n, argp);
+  }
+  if (s != KQ_OK) return s;
+  argmax_final_kernel<<<(unsigned)m, 256, 0, st>>>(argp, a.parts, tokens);
+  return kq_check_launch(BITS == 4 ? "kq_linear_argmax_int4" : "kq_linear_argmax_int8");
+}
+
+int check_argmax_args(const float* x, int64_t m, int64_t ldx, const void* wq, const void* sc,
+                      const float* logits, int64_t ldl, int64_t n, int64_t k, const int64_t* tokens) {
+  KQ_REQUIRE(x != nullptr && wq != nullptr && sc != nullptr && tokens != nullptr, "null pointer argument");
+  KQ_REQUIRE(m > 0 && n > 0 && k > 0, "empty linear");
+  KQ_REQUIRE(m <= 65535, "more than 65535 rows");
+  KQ_REQUIRE(n <= 0x7fffffff, "out_features beyond int32 indices");
+  KQ_REQUIRE(ldx >= k, "ldx smaller than in_features");
+  KQ_REQUIRE(logits == nullptr || ldl >= n, "ldl smaller than out_features");
+  return KQ_OK;
+}
+
+}  // namespace
+
+extern "C" size_t kq_linear_argmax_workspace_bytes(int scheme, int64_t m, int64_t n, int64_t k,
+                                                   int64_t group_size) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  if (scheme == 8) return arg_layout(make_plan(8, m, n, k, 0, k), m, n).total;
+  if (group_size <= 0) return 0;
+  const int64_t kp = (k + group_size - 1) / group_size * group_size;
+  return arg_layout(make_plan(4, m, n, k, group_size, kp), m, n).total;
+}
+
+extern "C" int kq_linear_argmax_int8(const float* x, int64_t m, int64_t ldx, const int8_t* payload,
+                                     const uint16_t* scales, const float* bias, float* logits,
+                                     int64_t ldl, int64_t n, int64_t k, int64_t* tokens, void* ws,
+                                     size_t ws_bytes, kq_stream_t stream) {
+  if (int s = check_argmax_args(x, m, ldx, payload, scales, logits, ldl, n, k, tokens)) return s;
+  const Plan p = make_plan(8, m, n, k, 0, k);
+  return linear_argmax<8>(p, x, m, ldx, reinterpret_cast<const uint8_t*>(payload), scales, k, 1, 1,
+                          bias, logits, ldl, n, k, tokens, ws, ws_bytes, kq_stream(stream));
+}
+
+extern "C" int kq_linear_argmax_int4(const float* x, int64_t m, int64_t ldx, const uint8_t* payload,
+                                     const uint16_t* scales, int64_t g, int64_t kp, const float* bias,
+                                     float* logits, int64_t ldl, int64_t n, int64_t k, int64_t* tokens,
+                                     void* ws, size_t ws_bytes, kq_stream_t stream) {
+  if (int s = check_argmax_args(x, m, ldx, payload, scales, logits, ldl, n, k, tokens)) return s;
+  KQ_REQUIRE(g > 0 && g % 2 == 0, "group_size must be a positive even integer");
+  KQ_REQUIRE(kp % g == 0 && kp >= k && kp - k < g, "inconsistent in_features_padded");
+  const Plan p = make_plan(4, m, n, k, g, kp);
+  return linear_argmax<4>(p, x, m, ldx, payload, scales, kp / 2, g, kp / g, bias, logits, ldl, n, k,
+                          tokens, ws, ws_bytes, kq_stream(stream));
 }

@@ -58,6 +58,7 @@ __all__ = [
     "QuantizedLinear",
     "concat_quantized",
     "FusedQuantizedLinear",
+    "quantized_linear_argmax",
 ]
 
 
@@ -321,6 +322,63 @@ def quantized_linear(x: torch.Tensor, qw: QuantizedWeight,
                 in_features, _lib.ptr(ws), nbytes, stream))
     y = y.reshape(*x.shape[:-1], out_features)
     return y if out_dtype == torch.float32 else y.to(out_dtype)
+
+
+def quantized_linear_argmax(x: torch.Tensor, qw: QuantizedWeight,
+                            bias: Optional[torch.Tensor] = None, return_logits: bool = False):
+    """Greedy token per row of ``F.linear(x, qw.dequantize(), bias)``: the
+    lm_head projection (engine/model.py:151) and ``logits.argmax()``
+    (:187, :200; first index of the maximum, a NaN counts as the maximum)
+    in one call.  The skinny kernel reduces each tile's logits to a partial
+    argmax in its epilogue; the logits are written only when
+    ``return_logits`` is set.  Returns int64 tokens of shape ``x.shape[:-1]``
+    (and the fp32 logits)."""
+    _lib.require_device(x, "input")
+    out_features, in_features = qw.original_shape
+    if x.shape[-1] != in_features:
+        raise RuntimeError(
+            f"mat1 and mat2 shapes cannot be multiplied "
+            f"({x.numel() // max(x.shape[-1], 1)}x{x.shape[-1]} and {in_features}x{out_features})")
+    if x.device != qw.payload.device:
+        raise RuntimeError(f"input on {x.device} but weight on {qw.payload.device}")
+    lib = _lib.load()
+    x2 = x.reshape(-1, in_features)
+    if x2.dtype != torch.float32:
+        x2 = x2.to(torch.float32)
+    if x2.stride(1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < in_features):
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    tokens = torch.empty((m,), dtype=torch.int64, device=x.device)
+    logits = (torch.empty((m, out_features), dtype=torch.float32, device=x.device)
+              if return_logits else None)
+    if m > 0:
+        b = None
+        if bias is not None:
+            b = bias.detach()
+            if b.dtype != torch.float32 or not b.is_contiguous():
+                b = b.to(torch.float32).contiguous()
+        ldx = x2.stride(0) if m > 1 else in_features
+        stream = _lib.stream_of(x2)
+        lp = _lib.ptr(logits)
+        if qw.scheme == "int8_per_channel":
+            nbytes = lib.kq_linear_argmax_workspace_bytes(8, m, out_features, in_features, 0)
+            ws = _lib.workspace(x.device, stream, nbytes)
+            _lib.check(lib.kq_linear_argmax_int8(
+                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), _lib.ptr(b),
+                lp, out_features, out_features, in_features, tokens.data_ptr(), _lib.ptr(ws),
+                nbytes, stream))
+        else:
+            g = qw.group_size
+            nbytes = lib.kq_linear_argmax_workspace_bytes(4, m, out_features, in_features, g)
+            ws = _lib.workspace(x.device, stream, nbytes)
+            _lib.check(lib.kq_linear_argmax_int4(
+                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), g,
+                qw.in_features_padded, _lib.ptr(b), lp, out_features, out_features, in_features,
+                tokens.data_ptr(), _lib.ptr(ws), nbytes, stream))
+    tokens = tokens.reshape(x.shape[:-1])
+    if return_logits:
+        return tokens, logits.reshape(*x.shape[:-1], out_features)
+    return tokens
 
 
 # ---------------------------------------------------------------------- #

@@ -69,6 +69,10 @@ def test_workspace_query_is_host_only():
     lambda L: L.kq_linear_int8(1, 1, 10, 1, 1, None, 1, 20, 20, 100, None, 0, None),
     lambda L: L.kq_linear_int4(1, 1, 128, 1, 1, 128, 100, None, 1, 20, 20, 100, None, 0, None),
     lambda L: L.kq_linear_int4(1, 1, 128, 1, 1, 3, 128, None, 1, 20, 20, 128, None, 0, None),
+    lambda L: L.kq_linear_argmax_int8(1, 1, 100, 1, 1, None, None, 0, 20, 100, None, None, 0, None),
+    lambda L: L.kq_linear_argmax_int8(1, 70000, 100, 1, 1, None, None, 0, 20, 100, 1, None, 0, None),
+    lambda L: L.kq_linear_argmax_int8(1, 1, 100, 1, 1, None, 1, 10, 20, 100, 1, None, 0, None),
+    lambda L: L.kq_linear_argmax_int4(1, 1, 128, 1, 1, 5, 130, None, None, 0, 20, 128, 1, None, 0, None),
 ])
 def test_argument_errors_are_reported_before_launch(call):
     lib = _lib.load()
@@ -84,6 +88,16 @@ def test_missing_workspace_is_reported():
     assert st == _lib.KQ_ERR_WORKSPACE
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.check(st)
+
+
+def test_argmax_needs_its_workspace():
+    lib = _lib.load()
+    # partial argmax pairs of the 16-column tiles: 8016 x 8 bytes at M = 1 (256-byte rounded)
+    assert lib.kq_linear_argmax_workspace_bytes(4, 1, 128256, 4096, 128) == (8016 * 8 + 255) // 256 * 256
+    # GEMM path: linear workspace + partials + a logits buffer
+    assert lib.kq_linear_argmax_workspace_bytes(8, 32, 1000, 256, 0) > 32 * 1000 * 4
+    st = lib.kq_linear_argmax_int8(1, 1, 4096, 1, 1, None, None, 0, 128256, 4096, 1, None, 0, None)
+    assert st == _lib.KQ_ERR_WORKSPACE
 
 
 def test_status_mapping():
@@ -169,6 +183,9 @@ def test_header_cites_reference_for_every_compute_entry_point():
                  "kq_linear_int8", "kq_linear_int4", "kq_check_finite"):
         block = text[:text.index(name + "(")].rsplit("/*", 1)[-1]
         assert "engine/quantization.py" in block, name
+    for name in ("kq_linear_argmax_int8", "kq_linear_argmax_int4"):
+        block = text[:text.index(name + "(")].rsplit("/*", 1)[-1]
+        assert "engine/model.py" in block, name
 
 
 def _oracle_qw(w, scheme):

@@ -10,7 +10,9 @@ INT4 G=128 on the GPU; h ~ N(0, 1) at M = 1 and M = 32.  Checks:
 * logits are within the linear-path bars (norm-wise and element-wise 1e-4)
   of the float64 value of the reference forward (exact dequantized weight);
 * the greedy token of every row equals the argmax of the float64 logits and of
-  the reference's own fp32 order (materialise w_hat, then an fp32 matmul).
+  the reference's own fp32 order (materialise w_hat, then an fp32 matmul),
+  both via torch.argmax over the logits and via the argmax fused into the
+  projection (quantized_linear_argmax).
   The smallest float64 top-2 gap over the rows is printed next to the largest
   logit error, so a run shows by how much the comparison clears a near-tie.
 """
@@ -22,7 +24,7 @@ import pytest
 import torch
 
 from kshipra_amd.quantization import (quantize_int4_per_group, quantize_int8_per_channel,
-                                      quantized_linear)
+                                      quantized_linear, quantized_linear_argmax)
 from oracle import quant
 
 pytestmark = pytest.mark.gpu
@@ -94,3 +96,6 @@ def test_lm_head_greedy_argmax(gpu, lm_head_weight, scheme):
         assert norm_err <= 1e-4 and elem_err <= 1e-4
         assert np.array_equal(tok, ref64_tok), (tok, ref64_tok)
         assert np.array_equal(tok, ref32_tok), (tok, ref32_tok)
+        # the same tokens from the argmax fused into the projection
+        fused = quantized_linear_argmax(hx, qw).cpu().numpy()
+        assert np.array_equal(fused, ref64_tok), (fused, ref64_tok)
