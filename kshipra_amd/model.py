@@ -15,6 +15,9 @@ decoder that runs every projection through ``QuantizedLinear`` on the GPU.
   attention over a contiguous KV cache and the fp32 lm_head are plain torch
   ops on the same device and stream.  With ``fuse=True`` q/k/v and gate/up run
   as one ``FusedQuantizedLinear`` launch each (same weights, row-stacked).
+  ``lm_head_scheme="int8"|"int4"`` quantizes the vocab projection too (the
+  reference keeps it fp32) and takes each greedy token from the argmax fused
+  into that projection.
 
 Weight dict keys (HF naming): ``embed_tokens.weight``, ``norm.weight``,
 ``lm_head.weight``, ``layers.{i}.{q,k,v,o,gate,up,down}_proj.weight``,
@@ -32,7 +35,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .quantization import FusedQuantizedLinear, QuantizedLinear
+from .quantization import (FusedQuantizedLinear, QuantizedLinear, quantize_int4_per_group,
+                           quantize_int8_per_channel, quantized_linear, quantized_linear_argmax)
 
 PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
@@ -92,13 +96,20 @@ class DecoderLM:
 
     def __init__(self, cfg: DecoderConfig, weights: Dict[str, torch.Tensor], scheme: str,
                  device: torch.device, group_size: int = 128, max_seq: int = 256,
-                 fuse: bool = False) -> None:
+                 fuse: bool = False, lm_head_scheme: Optional[str] = None) -> None:
         self.cfg = cfg
         self.device = device
         dev = lambda t: torch.as_tensor(t).to(device=device, dtype=torch.float32)
         self.embed = dev(weights["embed_tokens.weight"])
         self.norm = dev(weights["norm.weight"])
         self.lm_head = dev(weights["lm_head.weight"])
+        self.lm_head_q = None
+        if lm_head_scheme == "int8":
+            self.lm_head_q = quantize_int8_per_channel(self.lm_head)
+        elif lm_head_scheme == "int4":
+            self.lm_head_q = quantize_int4_per_group(self.lm_head, group_size)
+        elif lm_head_scheme is not None:
+            raise ValueError(f"lm_head_scheme must be None, 'int8' or 'int4', got {lm_head_scheme!r}")
         self.layers: List[Dict[str, object]] = []
         for li in range(cfg.num_layers):
             layer: Dict[str, object] = {
@@ -134,6 +145,15 @@ class DecoderLM:
     @torch.inference_mode()
     def forward(self, ids: List[int]) -> torch.Tensor:
         """Logits [L, vocab] for the next L tokens (engine/model.py:93-151)."""
+        h = self.hidden(ids)
+        if self.lm_head_q is not None:
+            return quantized_linear(h, self.lm_head_q)
+        return F.linear(h, self.lm_head)
+
+    @torch.inference_mode()
+    def hidden(self, ids: List[int]) -> torch.Tensor:
+        """Final-normed hidden states [L, hidden] (engine/model.py:93-150),
+        advancing the KV cache."""
         c = self.cfg
         L = len(ids)
         if self.pos + L > self.max_seq:
@@ -179,20 +199,29 @@ class DecoderLM:
             act = F.silu(gate) * up
             h = res + layer["down_proj"](act)
         self.pos = S
-        h = _rms_norm(h, self.norm, c.rms_norm_eps)
-        return F.linear(h, self.lm_head)
+        return _rms_norm(h, self.norm, c.rms_norm_eps)
+
+    @torch.inference_mode()
+    def _next(self, ids: List[int]) -> Tuple[int, torch.Tensor]:
+        """Greedy token after ``ids`` and its logits row (engine/model.py:187,200)."""
+        h = self.hidden(ids)[-1:]
+        if self.lm_head_q is not None:
+            tok, logits = quantized_linear_argmax(h, self.lm_head_q, return_logits=True)
+            return int(tok[0].item()), logits[0]
+        logits = F.linear(h, self.lm_head)[0]
+        return int(torch.argmax(logits).item()), logits
 
     @torch.inference_mode()
     def generate(self, prompt: List[int], max_new_tokens: int,
                  eos_token_id: Optional[int] = None) -> Tuple[List[int], List[torch.Tensor]]:
         """engine/model.py:153-205 greedy loop; returns (tokens, per-step logits)."""
         self.reset()
-        logits = self.forward(prompt)[-1]
-        toks, all_logits = [int(torch.argmax(logits).item())], [logits]
+        tok, logits = self._next(prompt)
+        toks, all_logits = [tok], [logits]
         for _ in range(1, max_new_tokens):
             if eos_token_id is not None and toks[-1] == eos_token_id:
                 break
-            logits = self.forward([toks[-1]])[-1]
-            toks.append(int(torch.argmax(logits).item()))
+            tok, logits = self._next([toks[-1]])
+            toks.append(tok)
             all_logits.append(logits)
         return toks, all_logits

@@ -16,7 +16,9 @@ decode steps, first-index argmax each step):
   computes the same with an online softmax over paged blocks).
 * Projections use the oracle's exact dequantized fp32 weights and an fp32
   GEMM, as ``QuantizedLinear.forward`` does (``engine/quantization.py:394-396``).
-  The lm_head is an unquantized fp32 linear (``engine/model.py:151``).
+  The lm_head is an unquantized fp32 linear (``engine/model.py:151``);
+  ``lm_head_scheme`` quantizes it the same way for the quantized-lm_head
+  extension (no counterpart in the reference, which keeps it fp32).
 
 Weights are a plain dict (see ``DecoderConfig`` and ``layer_keys``).
 """
@@ -85,9 +87,12 @@ class OracleDecoder:
     """fp32 CPU restatement of the decoder, with its own KV cache."""
 
     def __init__(self, cfg: DecoderConfig, weights: Dict[str, np.ndarray], scheme: str,
-                 group_size: int = 128) -> None:
+                 group_size: int = 128, lm_head_scheme=None) -> None:
         self.cfg = cfg
         self.w = weights
+        self.lm_head = weights["lm_head.weight"]
+        if lm_head_scheme is not None:
+            self.lm_head = quant.dequantize(quant.quantize(self.lm_head, lm_head_scheme, group_size))
         self.w_hat: List[Dict[str, np.ndarray]] = []
         for li in range(cfg.num_layers):
             d = {}
@@ -146,7 +151,7 @@ class OracleDecoder:
             h = res + self._lin(li, "down_proj", act.astype(np.float32))
         self.pos += L
         h = rms_norm(h, self.w["norm.weight"], c.rms_norm_eps)
-        return quant.linear_f32(h, self.w["lm_head.weight"]).astype(np.float32)
+        return quant.linear_f32(h, self.lm_head).astype(np.float32)
 
     def generate(self, prompt: List[int], max_new_tokens: int):
         """engine/model.py:153-205 greedy loop.  Returns (tokens, per-step logits)."""

@@ -21,14 +21,14 @@ from oracle import decoder as odec
 pytestmark = pytest.mark.gpu
 
 
-def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed, fuse=False):
+def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed, fuse=False, lm_head_scheme=None):
     w = decoder_weights(cfg_dict, seed=seed)
     ocfg = odec.DecoderConfig(**cfg_dict)
     gcfg = DecoderConfig(**cfg_dict)
     gpu_lm = DecoderLM(gcfg, {k: torch.from_numpy(v) for k, v in w.items()}, scheme, gpu,
-                       max_seq=len(prompt) + new_tokens + 1, fuse=fuse)
+                       max_seq=len(prompt) + new_tokens + 1, fuse=fuse, lm_head_scheme=lm_head_scheme)
     toks_g, logits_g = gpu_lm.generate(prompt, new_tokens)
-    oracle_lm = odec.OracleDecoder(ocfg, w, scheme)
+    oracle_lm = odec.OracleDecoder(ocfg, w, scheme, lm_head_scheme=lm_head_scheme)
     toks_o, logits_o = oracle_lm.generate(prompt, new_tokens)
     worst, min_gap = 0.0, np.inf
     for lg, lo in zip(logits_g, logits_o):
@@ -36,7 +36,8 @@ def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed, fuse=False):
         worst = max(worst, float(np.abs(lg - lo).max() / np.abs(lo).max()))
         top2 = np.sort(lo)[-2:]
         min_gap = min(min_gap, float(top2[1] - top2[0]))
-    print(f"[{scheme} L={cfg_dict['num_layers']} prompt={len(prompt)} fuse={fuse}] tokens {toks_g} "
+    print(f"[{scheme} L={cfg_dict['num_layers']} prompt={len(prompt)} fuse={fuse} "
+          f"lm_head={lm_head_scheme}] tokens {toks_g} "
           f"logit rel dev {worst:.3e} min top-2 gap {min_gap:.3e}", flush=True)
     assert toks_g == toks_o
     assert worst < 1e-3
@@ -53,6 +54,15 @@ def test_qwen05b_shaped_greedy_tokens(gpu, scheme):
 def test_qwen05b_shaped_fused_projections(gpu, scheme):
     """Same model with q/k/v and gate/up each run as one fused launch."""
     _greedy_parity(gpu, QWEN05B, scheme, [1, 42, 100, 201, 7, 999], 8, seed=0, fuse=True)
+
+
+@pytest.mark.parametrize("scheme", ["int4", "int8"])
+def test_qwen05b_shaped_quantized_lm_head(gpu, scheme):
+    """Fused projections plus a quantized lm_head whose greedy token comes from
+    the argmax fused into the projection; the oracle quantizes its lm_head the
+    same way."""
+    _greedy_parity(gpu, QWEN05B, scheme, [1, 42, 100, 201, 7, 999], 8, seed=0, fuse=True,
+                   lm_head_scheme=scheme)
 
 
 @pytest.mark.parametrize("scheme", ["int4", "int8"])
