@@ -35,8 +35,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .quantization import (FusedQuantizedLinear, QuantizedLinear, quantize_int4_per_group,
-                           quantize_int8_per_channel, quantized_linear, quantized_linear_argmax)
+from .quantization import (FusedQuantizedLinear, QuantizedLinear, QuantizedWeight,
+                           quantize_int4_per_group, quantize_int8_per_channel, quantized_linear,
+                           quantized_linear_argmax)
 
 PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
@@ -96,7 +97,12 @@ class DecoderLM:
 
     def __init__(self, cfg: DecoderConfig, weights: Dict[str, torch.Tensor], scheme: str,
                  device: torch.device, group_size: int = 128, max_seq: int = 256,
-                 fuse: bool = False, lm_head_scheme: Optional[str] = None) -> None:
+                 fuse: bool = False, lm_head_scheme: Optional[str] = None,
+                 quantized: Optional[Dict[str, "QuantizedWeight"]] = None) -> None:
+        """``quantized``: name (``layers.{i}.{proj}``) -> QuantizedWeight already
+        on ``device`` (e.g. from kshipra_amd.checkpoint.load_quantized_weights);
+        those projections are used as they are and their float weights are not
+        needed in ``weights``."""
         self.cfg = cfg
         self.device = device
         dev = lambda t: torch.as_tensor(t).to(device=device, dtype=torch.float32)
@@ -119,6 +125,13 @@ class DecoderLM:
             for p in PROJ:
                 out_f, in_f = cfg.proj_shape(p)
                 bias_key = f"layers.{li}.{p}.bias"
+                if quantized is not None and f"layers.{li}.{p}" in quantized:
+                    qw = quantized[f"layers.{li}.{p}"]
+                    if tuple(qw.original_shape) != (out_f, in_f):
+                        raise ValueError(f"layers.{li}.{p}: shape {qw.original_shape} != {(out_f, in_f)}")
+                    layer[p] = QuantizedLinear.from_quantized(
+                        qw, dev(weights[bias_key]) if bias_key in weights else None)
+                    continue
                 lin = nn.Linear(in_f, out_f, bias=bias_key in weights, device=device)
                 with torch.no_grad():
                     lin.weight.copy_(dev(weights[f"layers.{li}.{p}.weight"]))
@@ -134,6 +147,17 @@ class DecoderLM:
         self.inv_freq = (1.0 / (cfg.rope_theta ** exps)).to(device)
         self.max_seq = max_seq
         self.reset()
+
+    def quantized_weights(self) -> Dict[str, "QuantizedWeight"]:
+        """name (``layers.{i}.{proj}``) -> QuantizedWeight of every projection
+        (per projection: build with ``fuse=False`` to export)."""
+        out = {}
+        for li, layer in enumerate(self.layers):
+            for p in PROJ:
+                if p not in layer:
+                    raise ValueError("fused projections: build with fuse=False to export")
+                out[f"layers.{li}.{p}"] = layer[p].weight
+        return out
 
     def reset(self) -> None:
         c = self.cfg

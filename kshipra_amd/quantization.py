@@ -412,6 +412,23 @@ class QuantizedLinear(nn.Module):
         else:
             self.bias = None
 
+    @classmethod
+    def from_quantized(cls, qw: QuantizedWeight, bias: Optional[torch.Tensor] = None) -> "QuantizedLinear":
+        """A module around an already quantized weight (e.g. loaded from disk:
+        kshipra_amd.checkpoint), without the float original."""
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.out_features, self.in_features = qw.original_shape
+        self.scheme = "int8" if qw.scheme == "int8_per_channel" else "int4"
+        self.weight = qw
+        if bias is not None:
+            if bias.shape != (self.out_features,):
+                raise QuantizationError(f"bias shape {tuple(bias.shape)} != ({self.out_features},)")
+            self.register_buffer("bias", bias.detach().clone())
+        else:
+            self.bias = None
+        return self
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return quantized_linear(x, self.weight, self.bias)
 
