@@ -4,25 +4,29 @@ Headline workload: one Llama-3-8B decode step at M = 1 through all 32 layers x
 7 projections (q, k, v, o, gate, up, down) with INT4 G=128 weights, fp32
 activations -- every projection a distinct weight (3.6 GB INT4 / 7.0 GB INT8
 resident in HBM, far beyond the 256 MB MALL, so no repeat read is a cache hit).
-The 224 fused dequant-GEMV launches of a step are captured once in a HIP graph
-and replayed; ``value`` is algorithmic bytes (payload + scales + x + y) per
-step over the measured step time.
+As the decoder runs it, q/k/v and gate/up are each one dequant-GEMV launch over
+their row-stacked weights (4 launches per layer, 128 per step); the step is
+captured once in a HIP graph and replayed.  ``value`` is algorithmic bytes
+(payload + scales + x + y) per step over the measured step time.
 
 Also reported (same JSON line):
-  * INT8 per-channel M = 1 sweep (same shapes);
+  * the same step with 7 separate launches per layer (224 per step);
+  * INT8 per-channel M = 1 sweeps (same shapes);
   * per-projection GB/s (events around graphs of 32 same-shape launches);
-  * skinny M = 8 / 32 / 64 sweeps (continuous-batching decode);
+  * skinny / tiled M = 8 / 32 / 64 sweeps (continuous-batching decode);
   * INT4 prefill-chunk GEMM TFLOP/s (X [512 x 4096] through gate/up
     [14336 x 4096], then [512 x 14336] through down);
   * lm_head [128256 x 4096] INT8 / INT4 at M = 1 and 32: the GEMV alone,
     followed by torch.argmax, and with the greedy argmax fused into it;
-  * ``roofline``: the dominant kernel (gate/up projection dequant-GEMV) vs the
-    8 TB/s HBM peak;
+  * ``roofline``: the kernel that dominates the headline step (the fused
+    gate/up dequant-GEMV, [28672 x 4096]) vs the 8 TB/s HBM peak, with its
+    HBM traffic from the rocprofv3 counter summary under profiles/;
   * ``cpu_baseline``: the oracle's restatement of the reference forward
     (materialise w_hat = q * s in fp32, then one fp32 BLAS GEMV) timed on this
     host's cores over one layer (7 projections).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--eager] [--quick]
+                       [--only all|prefill|lm_head]
 """
 
 from __future__ import annotations
@@ -333,6 +337,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
     ap.add_argument("--layers", type=int, default=LAYERS,
                     help="layers in the sweep (fewer only for counter runs; the headline uses 32)")
+    ap.add_argument("--only", choices=("all", "prefill", "lm_head"), default="all",
+                    help="profiling aid: run one section and print its figures only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: the quantized-linear path runs on a single GPU "
@@ -342,26 +348,36 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     t_all = time.time()
+    if args.only != "all":
+        if args.only == "prefill":
+            pf = prefill_tflops(dev, args.steps, args.warmup, args.eager)
+            print(json.dumps({"section": "int4_prefill_m512_mlp", "tflops": round(pf["tflops"], 1),
+                              "ms": round(pf["ms"], 4), "gflop": round(pf["gflop"], 1),
+                              "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}))
+        else:
+            print(json.dumps({"section": "lm_head_128256x4096",
+                              "results": lm_head(dev, args.steps, args.warmup, args.eager)}))
+        return
 
     nl = args.layers
     int4 = build_layers("int4", dev, seed=1, nlayers=nl)
-    head = measure(int4, 1, dev, args.steps, args.warmup, args.eager)
-    print(f"# int4 M=1 sweep: {head['ms'] * 1e3:.1f} us/step, {head['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
-
-    breakdown = {"int4_m1": {"gbs": round(head["gbs"], 1), "us_per_step": round(head["ms"] * 1e3, 1)}}
+    # Headline: the decode step as the framework runs it, q/k/v and gate/up
+    # each one launch over their row-stacked weights (same bytes and outputs
+    # as the 7 separate projections, 4 launches per layer instead of 7).
+    head = measure(int4, 1, dev, args.steps, args.warmup, args.eager, names=[f[0] for f in FUSED])
+    print(f"# int4 M=1 fused sweep: {head['ms'] * 1e3:.1f} us/step, {head['gbs']:.0f} GB/s",
+          file=sys.stderr, flush=True)
+    sep = measure(int4, 1, dev, args.steps, args.warmup, args.eager)
+    breakdown = {"int4_m1_fused_qkv_gateup": {"gbs": round(head["gbs"], 1), "us_per_step": round(head["ms"] * 1e3, 1)},
+                 "int4_m1_separate_projections": {"gbs": round(sep["gbs"], 1), "us_per_step": round(sep["ms"] * 1e3, 1)}}
     per_proj = {}
-    for name, n, k in SHAPES:                         # 32 same-shape launches per graph
+    for name, n, k in SHAPES + [f for f in FUSED if f[0] in ("qkv", "gate_up")]:   # 32 same-shape launches per graph
         r = measure(int4, 1, dev, args.steps, args.warmup, args.eager, names=[name])
         per_proj[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2),
                           "bytes_per_launch": r["bytes"] // nl}
     breakdown["int4_m1_per_projection"] = per_proj
-    fz = measure(int4, 1, dev, args.steps, args.warmup, args.eager, names=[f[0] for f in FUSED])
-    breakdown["int4_m1_fused_qkv_gateup"] = {"gbs": round(fz["gbs"], 1), "us_per_step": round(fz["ms"] * 1e3, 1)}
-    for name in ("qkv", "gate_up"):
-        r = measure(int4, 1, dev, args.steps, args.warmup, args.eager, names=[name])
-        per_proj[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2),
-                          "bytes_per_launch": r["bytes"] // nl}
-    dom = max(("gate_proj", "up_proj", "down_proj"), key=lambda nm: per_proj[nm]["us_per_launch"])
+    # Roofline: the kernel that dominates the headline step's time.
+    dom = "gate_up"
     dom_bytes = per_proj[dom]["bytes_per_launch"]
     dom_us = per_proj[dom]["us_per_launch"]
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
@@ -374,16 +390,16 @@ def main():
     cpu = None
     if not args.quick:
         int8 = build_layers("int8", dev, seed=2, nlayers=nl)
-        r8 = measure(int8, 1, dev, args.steps, args.warmup, args.eager)
-        breakdown["int8_m1"] = {"gbs": round(r8["gbs"], 1), "us_per_step": round(r8["ms"] * 1e3, 1)}
-        per8 = {}
-        for name, n, k in SHAPES:
-            r = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[name])
-            per8[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2)}
-        breakdown["int8_m1_per_projection"] = per8
         fz8 = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[f[0] for f in FUSED])
         breakdown["int8_m1_fused_qkv_gateup"] = {"gbs": round(fz8["gbs"], 1),
                                                  "us_per_step": round(fz8["ms"] * 1e3, 1)}
+        r8 = measure(int8, 1, dev, args.steps, args.warmup, args.eager)
+        breakdown["int8_m1_separate_projections"] = {"gbs": round(r8["gbs"], 1), "us_per_step": round(r8["ms"] * 1e3, 1)}
+        per8 = {}
+        for name, n, k in SHAPES + [f for f in FUSED if f[0] in ("qkv", "gate_up")]:
+            r = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[name])
+            per8[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2)}
+        breakdown["int8_m1_per_projection"] = per8
         for m in (8, 32, 64):
             r = measure(int8, m, dev, max(args.steps // 2, 3), 1, args.eager)
             breakdown[f"int8_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
@@ -420,12 +436,14 @@ def main():
         "dtype": "int4xf32",
         "data": "synthetic: N(0, 0.02) weights drawn on the GPU and quantized by the HIP kernel; x ~ N(0, 1)",
         "config": {"workload": "Llama-3-8B decode step at M=1: 32 layers x (q,k,v,o,gate,up,down) "
-                               "INT4 G=128 dequant-GEMV, fp32 activations, one HIP graph per step",
+                               "INT4 G=128 dequant-GEMV, fp32 activations, q/k/v and gate/up each "
+                               "one launch over row-stacked weights (4 launches per layer), one "
+                               "HIP graph per step",
                    "layers": nl, "batch_m": 1, "scheme": "int4_per_group_g128",
                    "launch": "eager" if args.eager else "hip_graph",
                    "bytes_per_step": head["bytes"], "parallelism": "single_gpu"},
         "frac_of_hbm_peak": round(head["gbs"] / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": f"skinny dequant-GEMV INT4 ({dom}, M=1)",
+        "roofline": {"bound": "hbm", "kernel": f"skinny dequant-GEMV INT4 ({dom} [28672x4096], M=1)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,

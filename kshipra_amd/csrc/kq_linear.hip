@@ -855,9 +855,18 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
   const int64_t m = blockIdx.y, c0 = (int64_t)blockIdx.x * kArgChunk;
   float v = -__builtin_inff();
   int vi = 0x7fffffff;
-  for (int64_t c = c0 + threadIdx.x; c < c0 + kArgChunk && c < N; c += 256) {
-    const float a = y[m * ldy + c];
-    if (arg_better(a, (int)c, v, vi)) { v = a; vi = (int)c; }
+  // All 16 loads of a thread are issued before any is compared (unrolled,
+  // column clamped into the row), so their latencies overlap.
+  float a[kArgChunk / 256];
+#pragma unroll
+  for (int j = 0; j < kArgChunk / 256; j++) {
+    const int64_t col = c0 + threadIdx.x + 256 * j;
+    a[j] = y[m * ldy + (col < N ? col : N - 1)];
+  }
+#pragma unroll
+  for (int j = 0; j < kArgChunk / 256; j++) {
+    const int64_t col = c0 + threadIdx.x + 256 * j;
+    if (col < N && arg_better(a[j], (int)col, v, vi)) { v = a[j]; vi = (int)col; }
   }
   arg_reduce16(v, vi);
 #pragma unroll
@@ -876,17 +885,26 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
 }
 
 // Row argmax, pass 2: block m reduces the row's `parts` partials to tokens[m].
-__global__ __launch_bounds__(256) void argmax_final_kernel(const int2* __restrict__ argp, int64_t parts,
-                                                           int64_t* __restrict__ tokens) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
+__global__ __launch_bounds__(1024) void argmax_final_kernel(const int2* __restrict__ argp, int64_t parts,
+                                                            int64_t* __restrict__ tokens) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
   const int64_t m = blockIdx.x;
   float v = -__builtin_inff();
   int vi = 0x7fffffff;
-  for (int64_t j = threadIdx.x; j < parts; j += 256) {
-    const int2 q = argp[m * parts + j];
-    const float a = __int_as_float(q.x);
-    if (arg_better(a, q.y, v, vi)) { v = a; vi = q.y; }
+  // Eight partials per thread per round, all loaded before any is compared.
+  for (int64_t j0 = threadIdx.x; j0 < parts; j0 += 8 * 1024) {
+    int2 q[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int64_t j = j0 + 1024 * u;
+      q[u] = argp[m * parts + (j < parts ? j : parts - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const float a = __int_as_float(q[u].x);
+      if (j0 + 1024 * u < parts && arg_better(a, q[u].y, v, vi)) { v = a; vi = q[u].y; }
+    }
   }
   arg_reduce16(v, vi);
 #pragma unroll
@@ -898,7 +916,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const int2* __restric
   if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = vi; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; w++)
+    for (int w = 1; w < 16; w++)
       if (arg_better(sv[w], si[w], v, vi)) { v = sv[w]; vi = si[w]; }
     tokens[m] = vi;
   }
@@ -1323,7 +1341,7 @@ int linear_argmax(const Plan& p, const float* x, int64_t m, int64_t ldx, const u
     if (s == KQ_OK) argmax_partial_kernel<<<dim3((unsigned)a.parts, (unsigned)m), 256, 0, st>>>(y, ldy, n, argp);
   }
   if (s != KQ_OK) return s;
-  argmax_final_kernel<<<(unsigned)m, 256, 0, st>>>(argp, a.parts, tokens);
+  argmax_final_kernel<<<(unsigned)m, 1024, 0, st>>>(argp, a.parts, tokens);
   return kq_check_launch(BITS == 4 ? "kq_linear_argmax_int4" : "kq_linear_argmax_int8");
 }
 
