@@ -240,6 +240,13 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 
   u32x4 raw[KS][NT];
   uint16_t sv[NT][KS];  // raw fp16 bits: converting at load time would force an early wait
+  // INT4 group scales go first: results return in issue order, so a scale
+  // issued after the weights would make the first unit's scaling wait for
+  // every weight load of the batch.
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], ub, ue, sv[t]);
+  }
   // Unconditional (a branch here would make every later wait conservative):
   // units past ue reload unit ue - 1, which is in [0, nunits) for every wave.
 #pragma unroll
@@ -248,10 +255,10 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 #pragma unroll
     for (int t = 0; t < NT; t++) raw[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + unit * 64);
   }
-  if constexpr (BITS == 4) {
-#pragma unroll
-    for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], ub, ue, sv[t]);
-  }
+  // Nothing that waits for the activation pre-loads may be scheduled above
+  // the weight loads (a conversion hoisted there delays every weight load of
+  // the wave by one activation-load latency).
+  __builtin_amdgcn_sched_barrier(0);
 
   const half8_t* a = xa;
   if constexpr (A_LDS) {
@@ -325,15 +332,15 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 
   for (int64_t u0 = ub; u0 < ue; u0 += KS) {
     if (u0 != ub) {
+      if constexpr (BITS == 4) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], u0, ue, sv[t]);
+      }
 #pragma unroll
       for (int u = 0; u < KS; u++) {
         const int64_t unit = u0 + u < ue ? u0 + u : ue - 1;
 #pragma unroll
         for (int t = 0; t < NT; t++) raw[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + unit * 64);
-      }
-      if constexpr (BITS == 4) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], u0, ue, sv[t]);
       }
     }
 #pragma unroll
