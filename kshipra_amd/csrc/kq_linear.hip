@@ -229,7 +229,9 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
       const int e = lane + 64 * j;
       const int T = tb + (e >> 2), q4 = e & 3;
       pre_ok[j] = xvec && T < te && kstep_col0<BITS>(T, q4) + 8 <= K;
-      const float* src = x + (pre_ok[j] ? kstep_col0<BITS>(T, q4) : 0);
+      // A skipped entry reads 32 bytes of the payload instead (rows are at
+      // least 64 bytes; x may hold fewer than 8 values).
+      const float* src = pre_ok[j] ? x + kstep_col0<BITS>(T, q4) : reinterpret_cast<const float*>(wq);
       xa4[j] = reinterpret_cast<const float4*>(src)[0];
       xb4[j] = reinterpret_cast<const float4*>(src)[1];
     }
@@ -1017,6 +1019,7 @@ constexpr int64_t kSkinnyMinWaves = 2048;      // 8 waves per CU across 256 CUs
 constexpr int64_t kSkinnyMaxTotalWaves = 12288; // 48 per CU
 constexpr int kSkinnyNTMinM = 2;                // several 16-column tiles per workgroup from this M
 constexpr int64_t kSkinnyMinGroups = 192;
+constexpr int64_t kSkinnyOneRound = 4096;       // waves resident at once (4 per SIMD x 1024 SIMDs)
 constexpr int64_t kSkinnyLdsA = 64 * 1024;   // activation bytes staged in LDS by the workgroup
 constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
@@ -1087,6 +1090,25 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
     if ((int64_t)p.waves * best_pw < p.nunits)          // long K: several KS-unit batches
       p.per_wave = (p.nunits + p.waves - 1) / p.waves;
     p.ks = (int)std::min<int64_t>(best_pw, 16 / p.nt);
+    // M = 1: two tiles per wave in 4-unit batches and 8 waves per workgroup
+    // halve the activation staging per column (it reads all of x per
+    // workgroup) without fattening the waves, when that keeps >= 192
+    // workgroups and fits one round of resident waves.  Measured on the
+    // Llama-3-8B shapes: gate / up and q+k+v gain 0.5-1.6 us per launch;
+    // launches needing a second round of waves (gate+up) or leaving CUs idle
+    // (o_proj, down_proj) lose.
+    if (m == 1) {
+      int64_t pw2 = 1;
+      while (pw2 * 8 < p.nunits) pw2 *= 2;
+      const int64_t wpg = (p.nunits + pw2 - 1) / pw2;
+      const int64_t groups = ((n + 15) / 16 + 1) / 2;
+      if (pw2 >= 4 && wpg <= 8 && groups >= kSkinnyMinGroups && groups * wpg <= kSkinnyOneRound) {
+        p.nt = 2;
+        p.per_wave = pw2;
+        p.waves = (int)wpg;
+        p.ks = 4;
+      }
+    }
     p.svec = bits == 4 && p.per_wave % p.ks == 0 && (kp / 128) % p.ks == 0;
     // An odd pitch puts the four lane quads of an LDS row in different banks;
     // column nT is a pad column (written with unused values, never read).

@@ -24,7 +24,7 @@ import torch.nn as nn
 from cases import LLAMA3_8B_SHAPES, gaussian, with_outliers
 from kshipra_amd.quantization import (FusedQuantizedLinear, QuantizedLinear,
                                       quantize_int4_per_group, quantize_int8_per_channel,
-                                      quantized_linear)
+                                      quantized_linear, quantized_linear_argmax)
 from oracle import quant
 
 pytestmark = pytest.mark.gpu
@@ -83,6 +83,30 @@ def _run(gpu, m, n, k, scheme, g=128, bias=True, seed=0, outliers=False):
 def test_skinny_paths(gpu, scheme, m):
     _run(gpu, m, 272, 896, scheme, seed=m)              # K = 896: 7 groups / 14 windows
     _run(gpu, m, 100, 4864, scheme, seed=m + 50)        # N % 16 != 0, odd unit counts
+
+
+@pytest.mark.parametrize("n,k,scheme", [
+    (6144, 4096, "int4"), (6150, 4096, "int8"),   # q+k+v; last workgroup with one partial tile
+    (14336, 4096, "int8"), (6200, 4096, "int4"),  # gate / up; N % 32 == 24
+])
+def test_m1_two_tile_waves(gpu, n, k, scheme):
+    """M = 1 with two 16-column tiles per wave (8-wave workgroups): bias and
+    no bias, aligned and unaligned activations, and the fused greedy argmax
+    over the same launch shape."""
+    w = gaussian((n, k), seed=n + k)
+    b = gaussian((n,), seed=n + k + 1)
+    wt = torch.from_numpy(w).to(gpu)
+    qw = quantize_int8_per_channel(wt) if scheme == "int8" else quantize_int4_per_group(wt, 128)
+    del wt
+    xs = torch.from_numpy(gaussian((1, k + 1), seed=n + k + 2, std=1.0)).to(gpu)
+    for name, x, bias in (("aligned", xs[:, :k].contiguous(), b), ("unaligned", xs[:, 1:], None)):
+        bt = None if bias is None else torch.from_numpy(bias).to(gpu)
+        y = quantized_linear(x, qw, bt)
+        torch.cuda.synchronize()
+        y64, mag = _reference(x.cpu().numpy(), w, scheme, 128, bias)
+        _compare(y, y64, mag, f"two-tile {scheme} n={n} k={k} {name}")
+        tok = quantized_linear_argmax(x, qw, bt).reshape(-1).cpu()
+        assert torch.equal(tok, y.argmax(dim=-1).reshape(-1).cpu()), name
 
 
 @pytest.mark.parametrize("scheme", ["int8", "int4"])
