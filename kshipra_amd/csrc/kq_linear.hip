@@ -182,15 +182,27 @@ __device__ __forceinline__ void arg_reduce16(float& v, int& i) {
 template <int KS, int NT>
 constexpr int skinny_max_threads() { return KS * NT >= 16 ? 512 : 1024; }
 
-template <int BITS, int KS, int NT, bool A_LDS, bool HL, bool SVEC>
+// M1: instances for M == 1 exactly (one row: pre-load count and layout known
+// at compile time, no row stepping).  REM: activation entries may remain after
+// the pre-loads (unaligned or K-tail x, more entries than pre-load slots), so
+// the code loading them after the weights is compiled in; the host launches
+// REM = false instances only when the pre-loads cover every entry (a
+// possibly-taken block of loads behind the weights would make the compiler
+// wait for all weight loads before the first MFMA).
+// wq / sc are deliberately not __restrict__: loads through restrict read-only
+// kernel arguments count as invariant and may be sunk past the asm ordering
+// fences, which moved the first batch's weight loads behind the staging.
+template <int BITS, int KS, int NT, bool A_LDS, bool HL, bool SVEC, bool M1, bool REM>
 __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
-    const float* __restrict__ x, int64_t ldx, int M, int64_t K, bool xvec,
-    const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
+    const float* __restrict__ x, int64_t ldx, int M_, int64_t K, bool xvec,
+    const uint8_t* wq, const uint16_t* sc, int64_t row_bytes,
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
     const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
     int2* __restrict__ argp) {
+  static_assert(!M1 || (A_LDS && HL && !REM), "single-row instances stage in LDS, pre-loads only");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int TPU = BITS == 4 ? 4 : 2;  // k-steps per unit
+  const int M = M1 ? 1 : M_;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwaves = blockDim.x >> 6;
@@ -215,25 +227,47 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
   // weights.  Then the first chunk of packed weights (and, for INT4, its group
   // scales) goes in flight, then the staging converts while HBM answers.
   // Each wave stages only the k-steps of its own units, [ub, ue) * TPU, so a
-  // wave-level sync replaces a workgroup barrier.  Lane l owns entries
-  // e = l + 64 j (k-step ub * TPU + e / 4, quad e % 4) with all M rows; the
-  // first PRE of them (row 0; one batch of KS units' worth) are loaded before
-  // the weights.
-  constexpr int PRE = KS * TPU / 16 < 1 ? 1 : (KS * TPU / 16 > 4 ? 4 : KS * TPU / 16);
+  // wave-level sync replaces a workgroup barrier.  Entries are numbered
+  // f = m * E + e over the M rows (e: k-step tb + e / 4, quad e % 4); lane l
+  // owns f = l + 64 j.  The first pre_n <= PRE of them (every row) are loaded
+  // before the weights; only entries past them (or unaligned / K-tail x) are
+  // loaded after the weights, where converting them waits for the weights.
+  // One row: PRE covers one batch of KS units, loaded unconditionally.
+  constexpr int PRE1 = KS * TPU / 16 < 1 ? 1 : (KS * TPU / 16 > 4 ? 4 : KS * TPU / 16);
+  constexpr int PRE = M1 ? PRE1 : 4;
   const int tb = (int)(ub * TPU), te = (int)(ue * TPU);
-  float4 xa4[PRE], xb4[PRE];
-  bool pre_ok[PRE];
+  const int E = (te - tb) * 4;
+  const int ntot = M * E;
+  const int pre_n = M1 ? PRE : ((ntot + 63) / 64 < PRE ? (ntot + 63) / 64 : PRE);
+  floatx4 xa4[PRE], xb4[PRE];
+  unsigned pre_mask = 0;  // bit j: entry lane + 64 j was pre-loaded
+  int pm[PRE], pe[PRE];   // its row and in-row index
   if constexpr (A_LDS) {
+    // (row, in-row index) of f = lane + 64 j, stepped without a division.
+    int m = 0, e = lane;
 #pragma unroll
     for (int j = 0; j < PRE; j++) {
-      const int e = lane + 64 * j;
-      const int T = tb + (e >> 2), q4 = e & 3;
-      pre_ok[j] = xvec && T < te && kstep_col0<BITS>(T, q4) + 8 <= K;
-      // A skipped entry reads 32 bytes of the payload instead (rows are at
-      // least 64 bytes; x may hold fewer than 8 values).
-      const float* src = pre_ok[j] ? x + kstep_col0<BITS>(T, q4) : reinterpret_cast<const float*>(wq);
-      xa4[j] = reinterpret_cast<const float4*>(src)[0];
-      xb4[j] = reinterpret_cast<const float4*>(src)[1];
+      if (j > 0) e += 64;
+      if constexpr (!M1) {
+        while (e >= E && m < M) { e -= E; m++; }
+      }
+      pm[j] = m;
+      pe[j] = e;
+    }
+#pragma unroll
+    for (int j = 0; j < PRE; j++) {
+      if (M1 || j < pre_n) {
+        const int f = lane + 64 * j;
+        const int m = pm[j], e = pe[j];
+        const int T = tb + (e >> 2), q4 = e & 3;
+        const bool ok = xvec && f < ntot && kstep_col0<BITS>(T, q4) + 8 <= K;
+        pre_mask |= (unsigned)ok << j;
+        // A skipped entry reads 32 bytes of the payload instead (rows are at
+        // least 64 bytes; x may hold fewer than 8 values).
+        const float* src = ok ? x + m * ldx + kstep_col0<BITS>(T, q4) : reinterpret_cast<const float*>(wq);
+        xa4[j] = reinterpret_cast<const floatx4*>(src)[0];
+        xb4[j] = reinterpret_cast<const floatx4*>(src)[1];
+      }
     }
   }
   // Keep these loads ahead of the weight loads (an IR-level ordering fence;
@@ -257,47 +291,60 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 #pragma unroll
     for (int t = 0; t < NT; t++) raw[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + unit * 64);
   }
-  // Nothing that waits for the activation pre-loads may be scheduled above
-  // the weight loads (a conversion hoisted there delays every weight load of
-  // the wave by one activation-load latency).
+  // Nothing that waits for the activation pre-loads may be placed above the
+  // weight loads (a conversion there delays every weight load of the wave by
+  // one activation-load latency): the pre-loaded registers pass through an
+  // empty asm statement here, after the weight loads, so their wait and
+  // conversion come after it.
+  __asm__ volatile("" ::: "memory");
+  if constexpr (A_LDS) {
+#pragma unroll
+    for (int j = 0; j < PRE; j++) {
+      if (M1 || j < pre_n) __asm__ volatile("" : "+v"(xa4[j]), "+v"(xb4[j]));
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   const half8_t* a = xa;
   if constexpr (A_LDS) {
     half8_t* la = reinterpret_cast<half8_t*>(smem);
-    // Unconditional: a lane without a valid pre-load writes its (unused)
-    // values to the pad column T = nT, which no lane reads.  A branch here
-    // would let the compiler sink the pre-loads behind the weight loads.
+    // A lane without a valid pre-load writes its (unused) values to the pad
+    // column T = nT of row 0, which no lane reads.
 #pragma unroll
     for (int j = 0; j < PRE; j++) {
-      const int e = lane + 64 * j;
-      const float raw8[8] = {xa4[j].x, xa4[j].y, xa4[j].z, xa4[j].w,
-                             xb4[j].x, xb4[j].y, xb4[j].z, xb4[j].w};
-      half8_t hi, lo;
-      stage_convert<BITS>(raw8, hi, lo);
-      skinny_store<HL>(la, M, pitch, pre_ok[j] ? tb + (e >> 2) : nT, e & 3, 0, hi, lo);
+      if (M1 || j < pre_n) {
+        const int m = pm[j], e = pe[j];
+        const bool ok = (pre_mask >> j) & 1;
+        const float raw8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
+                               xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
+        half8_t hi, lo;
+        stage_convert<BITS>(raw8, hi, lo);
+        skinny_store<HL>(la, M, pitch, ok ? tb + (e >> 2) : nT, e & 3, ok ? m : 0, hi, lo);
+      }
     }
-    // Everything else (rows m > 0, further entries, unaligned x): loaded now,
-    // after the weights are in flight.
-    for (int e = lane; e < (te - tb) * 4; e += 64) {
-      const int T = tb + (e >> 2), q4 = e & 3;
-      bool pre = false;
-#pragma unroll
-      for (int j = 0; j < PRE; j++) pre = pre || (e == lane + 64 * j && pre_ok[j]);
-      // Rows in groups of four: the four rows' loads are issued together
-      // (row index clamped into [0, M), extra rows not stored), so their
-      // latencies overlap instead of adding up.
-      for (int m0 = pre ? 1 : 0; m0 < M; m0 += 4) {
+    // Everything else: four entries per lane at a time, their loads issued
+    // together so the latencies overlap.  Skipped (wave-uniformly) when the
+    // pre-loads covered every entry, so no wait for the weights is emitted.
+    if (REM && (ntot > 64 * pre_n || !xvec || (K & 7) != 0)) {
+      for (int j0 = 0; 64 * j0 < ntot; j0 += 4) {
         float raw8[4][8];
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          stage_load<BITS>(x, ldx, M, K, T, q4, m0 + r < M ? m0 + r : M - 1, xvec, raw8[r]);
+        bool need[4];
+        int mm[4], ee[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          if (m0 + r < M) {
+          const int j = j0 + r, f = lane + 64 * j;
+          need[r] = f < ntot && !(j < pre_n && ((pre_mask >> j) & 1));
+          mm[r] = need[r] ? f / E : 0;
+          ee[r] = need[r] ? f - mm[r] * E : 0;
+          // row M: stage_load returns zeros without reading
+          stage_load<BITS>(x, ldx, M, K, tb + (ee[r] >> 2), ee[r] & 3, need[r] ? mm[r] : M, xvec, raw8[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (need[r]) {
             half8_t hi, lo;
             stage_convert<BITS>(raw8[r], hi, lo);
-            skinny_store<HL>(la, M, pitch, T, q4, m0 + r, hi, lo);
+            skinny_store<HL>(la, M, pitch, tb + (ee[r] >> 2), ee[r] & 3, mm[r], hi, lo);
           }
         }
       }
@@ -1020,7 +1067,9 @@ constexpr int64_t kSkinnyMaxTotalWaves = 12288; // 48 per CU
 constexpr int kSkinnyNTMinM = 2;                // several 16-column tiles per workgroup from this M
 constexpr int64_t kSkinnyMinGroups = 192;
 constexpr int64_t kSkinnyOneRound = 4096;       // waves resident at once (4 per SIMD x 1024 SIMDs)
-constexpr int64_t kSkinnyLdsA = 64 * 1024;   // activation bytes staged in LDS by the workgroup
+constexpr int64_t kSkinnyLdsA = 160 * 1024;  // LDS per CU (gfx950), all usable by one workgroup
+constexpr int64_t kSkinnyLdsSmall = 64 * 1024;  // staging this small never limits residency
+constexpr int64_t kCUs = 256;
 constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
 constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU
@@ -1113,7 +1162,16 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
     // An odd pitch puts the four lane quads of an LDS row in different banks;
     // column nT is a pad column (written with unused values, never read).
     p.pitch = (p.nT + 1) | 1;
-    p.a_lds = 128 * p.pitch * m <= kSkinnyLdsA;  // 2 halves x 16 B x 4 quads per entry
+    // Staged activations: 2 halves x 16 B x 4 quads per entry.  Above 64 KiB
+    // they limit how many workgroups a CU holds; stage in LDS then only if
+    // the whole grid is still resident at once (else a second round of
+    // workgroups waits: measured slower than staging by a pre-pass).
+    {
+      const int64_t abytes = 128 * p.pitch * m;
+      const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
+      p.a_lds = abytes <= kSkinnyLdsSmall ||
+                (abytes <= kSkinnyLdsA && (kSkinnyLdsA / abytes) * kCUs >= groups);
+    }
     if (!p.a_lds) p.pitch = p.nT;
     p.ws = p.a_lds ? 0 : (size_t)(128 * p.pitch * m);
     return p;
@@ -1145,14 +1203,14 @@ inline bool x_vectorizable(const float* x, int64_t ldx, int64_t k) {
   return (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 4 == 0) && k >= 8;
 }
 
-template <int BITS, bool LDS, bool HL, bool SVEC>
+template <int BITS, bool LDS, bool HL, bool SVEC, bool M1, bool REM>
 void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStream_t st,
                       const float* x, int64_t ldx, int64_t m, int64_t k, bool xvec,
                       const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                       const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n,
                       int2* argp) {
 #define KQ_SKINNY(KS_, NT_)                                                                   \
-  skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC><<<grid, block, shm, st>>>(                     \
+  skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC, M1, REM><<<grid, block, shm, st>>>(            \
       x, ldx, (int)m, k, xvec, wq, sc, row_bytes, ng, p.nunits, p.per_wave, (int)p.pitch, xa, \
       bias, y, ldy, n, argp)
   if (p.nt == 4) {
@@ -1197,21 +1255,39 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   const dim3 grid((unsigned)((n + 16 * p.nt - 1) / (16 * p.nt)));
   const dim3 block((unsigned)(64 * p.waves));
   const bool svec = p.svec && reinterpret_cast<uintptr_t>(sc) % (2 * p.ks) == 0;
-#define KQ_SKINNY_SV(LDS_, HL_)                                                                 \
+#define KQ_SKINNY_SV(LDS_, HL_, M1_, REM_)                                                      \
   do {                                                                                          \
-    if (svec) launch_skinny_ks<BITS, LDS_, HL_, true>(p, grid, block, shm, st, x, ldx, m, k,   \
-                                                      xvec, wq, sc, row_bytes, ng, xa, bias, y, \
-                                                      ldy, n, argp);                            \
-    else launch_skinny_ks<BITS, LDS_, HL_, false>(p, grid, block, shm, st, x, ldx, m, k, xvec,  \
-                                                  wq, sc, row_bytes, ng, xa, bias, y, ldy, n,   \
-                                                  argp);                                        \
+    if (svec)                                                                                   \
+      launch_skinny_ks<BITS, LDS_, HL_, true, M1_, REM_>(p, grid, block, shm, st, x, ldx, m, k, \
+                                                         xvec, wq, sc, row_bytes, ng, xa, bias, \
+                                                         y, ldy, n, argp);                      \
+    else                                                                                        \
+      launch_skinny_ks<BITS, LDS_, HL_, false, M1_, REM_>(p, grid, block, shm, st, x, ldx, m,   \
+                                                          k, xvec, wq, sc, row_bytes, ng, xa,   \
+                                                          bias, y, ldy, n, argp);               \
   } while (0)
+  // Do the pre-loads (one batch of KS units at M = 1, else 4 entries per
+  // lane over all rows) cover every activation entry of every wave?  The
+  // single-row instances are used for INT4 (measured: INT8 runs as fast or
+  // faster through the general ones).
+  constexpr int kTpu = BITS == 4 ? 4 : 2;
+  const int pre1 = std::min(4, std::max(1, p.ks * kTpu / 16));
+  const bool aligned = xvec && k % 8 == 0;
+  const bool one_row = BITS == 4 && aligned && m == 1 && p.per_wave * kTpu <= 16 * pre1;
+  const bool covered = aligned && m * p.per_wave * kTpu <= 16 * 4;
   if (p.a_lds) {
-    if (p.hl) KQ_SKINNY_SV(true, true);
-    else KQ_SKINNY_SV(true, false);
+    if constexpr (BITS == 4) {
+      if (p.hl && one_row) {
+        KQ_SKINNY_SV(true, true, true, false);
+        return kq_check_launch("kq_linear_int4 (skinny)");
+      }
+    }
+    if (p.hl && covered) KQ_SKINNY_SV(true, true, false, false);
+    else if (p.hl) KQ_SKINNY_SV(true, true, false, true);
+    else KQ_SKINNY_SV(true, false, false, true);
   } else {
-    if (p.hl) KQ_SKINNY_SV(false, true);
-    else KQ_SKINNY_SV(false, false);
+    if (p.hl) KQ_SKINNY_SV(false, true, false, false);
+    else KQ_SKINNY_SV(false, false, false, false);
   }
 #undef KQ_SKINNY_SV
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");

@@ -47,8 +47,12 @@ def test_workspace_query_is_host_only():
     # M = 1 INT4 / INT8 on Llama-3-8B shapes: activations fit in LDS, no workspace
     assert lib.kq_linear_workspace_bytes(4, 1, 14336, 4096, 128) == 0
     assert lib.kq_linear_workspace_bytes(8, 1, 4096, 14336, 0) == 0
-    # M = 8, K = 4096: staged in the workspace, 4 bytes per activation
-    assert lib.kq_linear_workspace_bytes(8, 8, 4096, 4096, 0) == 4 * 8 * 4096
+    # M = 8, K = 4096: 132 KiB of staged activations per workgroup; 256
+    # workgroups (one per CU) stage in LDS, 448 (a second round) in the
+    # workspace, 4 bytes per activation; K = 14336 never fits in LDS
+    assert lib.kq_linear_workspace_bytes(8, 8, 4096, 4096, 0) == 0
+    assert lib.kq_linear_workspace_bytes(8, 8, 28672, 4096, 0) == 4 * 8 * 4096
+    assert lib.kq_linear_workspace_bytes(4, 8, 4096, 14336, 128) == 4 * 8 * 14336
     # GEMM path: M rounded up to the 64-row tile
     assert lib.kq_linear_workspace_bytes(4, 512, 14336, 4096, 128) == 4 * 512 * 4096
     assert lib.kq_linear_workspace_bytes(4, 100, 64, 256, 128) == 4 * 128 * 256
@@ -83,8 +87,8 @@ def test_argument_errors_are_reported_before_launch(call):
 
 def test_missing_workspace_is_reported():
     lib = _lib.load()
-    # M = 8, K = 4096 needs a workspace; pointers are never dereferenced
-    st = lib.kq_linear_int8(1, 8, 4096, 1, 1, None, 1, 4096, 4096, 4096, None, 0, None)
+    # M = 8, N = 28672, K = 4096 needs a workspace; pointers are never dereferenced
+    st = lib.kq_linear_int8(1, 8, 4096, 1, 1, None, 1, 28672, 28672, 4096, None, 0, None)
     assert st == _lib.KQ_ERR_WORKSPACE
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.check(st)
