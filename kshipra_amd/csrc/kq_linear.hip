@@ -470,6 +470,30 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Workgroup -> (m-tile, n-tile, K split).  Dispatch places block b on XCD
+// b % 8, so block b is renumbered r such that each XCD works on one
+// contiguous range of r.  r runs through bands of gm m-tiles: within a band
+// the m-tile varies fastest, then the n-tile, so one XCD's range touches gm
+// m-tiles of activations (sized by the host to stay in that XCD's L2) and
+// its weight columns are read by gm workgroups there.  The K split is the
+// slowest index.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void gemm_tile(int tiles_m, int tiles_n, int gm, int64_t& tm,
+                                          int64_t& tn, int64_t& z) {
+  const int64_t nblk = gridDim.x, b = blockIdx.x;
+  const int64_t xcd = b % 8, slot = b / 8, q8 = nblk / 8, rem = nblk % 8;
+  const int64_t r = xcd < rem ? xcd * (q8 + 1) + slot : rem * (q8 + 1) + (xcd - rem) * q8 + slot;
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  z = r / tiles;
+  const int64_t rt = r - z * tiles;
+  const int64_t grp = (int64_t)gm * tiles_n;
+  const int64_t band = rt / grp, rb = rt - band * grp;
+  const int64_t rows = gm < tiles_m - band * gm ? gm : tiles_m - band * gm;
+  tm = band * gm + rb % rows;
+  tn = rb / rows;
+}
+
+// ---------------------------------------------------------------------------
 // GEMM path: M > 16 (batched decode, prefill chunks).
 //
 // stage_planes_kernel converts x once per call into fp16 hi/lo MFMA operand
@@ -520,7 +544,7 @@ template <int BITS, int MTW, int NTW, int WN>
 __global__ __launch_bounds__(64 * WN) void gemm_kernel(
     const half8_t* __restrict__ planes, int64_t Mp, int64_t M,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
-    int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n,
+    int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n, int gm,
     const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
     float* __restrict__ part) {
   constexpr int BM = 16 * MTW;
@@ -538,11 +562,8 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
   // Tile order: consecutive blocks land on different XCDs, so give each XCD a
   // contiguous range of tiles (m fastest: the m-tiles of one n-tile share
   // their weight columns through that XCD's L2).
-  const int64_t nblk = gridDim.x, b = blockIdx.x;
-  const int64_t xcd = b % 8, slot = b / 8, q8 = nblk / 8, rem = nblk % 8;
-  const int64_t r = xcd < rem ? xcd * (q8 + 1) + slot : rem * (q8 + 1) + (xcd - rem) * q8 + slot;
-  const int64_t tm = r % tiles_m, rest = r / tiles_m;
-  const int64_t tn = rest % tiles_n, z = rest / tiles_n;
+  int64_t tm, tn, z;
+  gemm_tile(tiles_m, tiles_n, gm, tm, tn, z);
   const int64_t m0 = tm * BM;
   const int64_t n0 = (tn * WN + wave) * (16 * NTW);
   const int64_t sb = z * spz;
@@ -700,8 +721,8 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
 // Warp-specialized GEMM (prefill chunks): one producer wave moves each
 // stage's operand block (both planes) and the packed weight columns straight
 // from memory into an LDS ring of D stages with global_load_lds_dwordx4
-// (no registers, no conversion), D - 1 stages ahead of the math; four
-// consumer waves (64 x 64 tiles, BM = 64, BN = 256) only read LDS and run
+// (no registers, no conversion), D - 1 stages ahead of the math; NC
+// consumer waves (64 x 64 tiles: BM = 64, BN = 64 NC) only read LDS and run
 // MFMAs.  Synchronisation per stage: the producer waits (explicit vmcnt) for
 // the stage the consumers are about to read, then one s_barrier; the
 // producer's next DMA targets the slot the consumers finished a stage ago.
@@ -713,8 +734,13 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
 // 16-byte lane slot l holds what MFMA lane l needs (row n0 + 16 t + (l & 15),
 // bytes (l >> 4) * 16 of the stage's window r).
 // ---------------------------------------------------------------------------
-constexpr int kWsConsumers = 4;
-constexpr int kWsThreads = 64 * (kWsConsumers + 1);
+// Shapes (consumer waves of 64 columns, LDS ring depth): 4 consumers with a
+// 3-deep ring, or for INT4 grids that fill the GPU without a K split, 7
+// consumers (two math waves on most SIMDs, BN = 448) with a 2-deep ring
+// (measured 13 % faster there, slower elsewhere: partial 448-column tiles,
+// K splits).  INT8 windows need twice the weight ring: 4 consumers, 2 deep.
+constexpr int kWsNC = 4, kWsWideNC = 7;
+constexpr int64_t kWsWideMinTiles = 256;
 
 __device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
@@ -730,35 +756,33 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
   __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
 
-template <int BITS, int D>
-__global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
+template <int BITS, int D, int NC>
+__global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
     const half8_t* __restrict__ planes, int64_t Mp, int64_t M,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
-    int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n,
+    int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n, int gm,
     const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
     float* __restrict__ part) {
   constexpr int MTW = 4, NTW = 4, BM = 64;
   constexpr int PLANE = BM * 16;                        // entries per plane
   constexpr int RAWN = BITS == 4 ? 1 : 2;               // 64-byte windows per stage
   constexpr int ABLK = 2 * PLANE / 64;                  // 1 KB operand blocks per stage
-  constexpr int WBLK = kWsConsumers * NTW * RAWN;       // 1 KB weight blocks per stage
+  constexpr int WBLK = NC * NTW * RAWN;                 // 1 KB weight blocks per stage
   constexpr int SLOT = (ABLK + WBLK) * 64;              // 16-byte entries per slot
   constexpr int NDMA = ABLK + WBLK;                     // producer DMAs per stage
   static_assert(NDMA * (D - 2) < 64, "vmcnt range");
+  static_assert(D * SLOT * 16 <= 160 * 1024, "LDS ring exceeds 160 KiB");
   __shared__ u32x4 ring[D * SLOT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool producer = wave == kWsConsumers;
+  const bool producer = wave == NC;
   const int qd = lane >> 4, c = lane & 15;
 
-  const int64_t nblk = gridDim.x, b = blockIdx.x;
-  const int64_t xcd = b % 8, slot = b / 8, q8 = nblk / 8, rem = nblk % 8;
-  const int64_t r = xcd < rem ? xcd * (q8 + 1) + slot : rem * (q8 + 1) + (xcd - rem) * q8 + slot;
-  const int64_t tm = r % tiles_m, rest = r / tiles_m;
-  const int64_t tn = rest % tiles_n, z = rest / tiles_n;
+  int64_t tm, tn, z;
+  gemm_tile(tiles_m, tiles_n, gm, tm, tn, z);
   const int64_t m0 = tm * BM;
-  const int64_t nb = tn * kWsConsumers * 16 * NTW;      // first column of the workgroup
+  const int64_t nb = tn * NC * 16 * NTW;                // first column of the workgroup
   const int64_t sb = z * spz;
   const int64_t se = sb + spz < nstages ? sb + spz : nstages;
   const int64_t nst = se - sb;
@@ -774,7 +798,7 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
       dma16(planes + e, base + j * 64);
     }
 #pragma unroll
-    for (int w = 0; w < kWsConsumers; w++)
+    for (int w = 0; w < NC; w++)
 #pragma unroll
       for (int t = 0; t < NTW; t++) {
         const int64_t n = nb + 64 * w + 16 * t + (lane & 15);
@@ -834,47 +858,49 @@ __global__ __launch_bounds__(kWsThreads) void gemm_ws_kernel(
 #pragma unroll
       for (int rr = 0; rr < RAWN; rr++)
         wr[t][rr] = base[(ABLK + (wave * NTW + t) * RAWN + rr) * 64 + lane];
-    // The stage's B operands (4 k-steps x NTW tiles), converted once.
-    half8_t bw[4][NTW];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int t = 0; t < NTW; t++) {
-        if constexpr (BITS == 4) bw[i][t] = int4x8_to_half8(wr[t][0][i]);
-        else bw[i][t] = int8x8_to_half8(wr[t][i >> 1][2 * (i & 1)], wr[t][i >> 1][2 * (i & 1) + 1]);
-      }
     float sf[NTW];
     if constexpr (BITS == 4) {
 #pragma unroll
       for (int t = 0; t < NTW; t++) { sf[t] = f16_bits_to_f32(scur[t]); scur[t] = snx[t]; }
     }
-    // One 16-row m-tile at a time through all four k-steps: INT4 applies the
-    // group scale to that m-tile's partial sums while the next m-tile's
-    // MFMAs run, instead of draining every accumulator at the stage's end.
+    // k-step outer, m-tile inner: only one k-step's B operands are converted
+    // ahead of its MFMAs, so converting the next k-step (and reading its A
+    // fragments) overlaps the current k-step's 8 MTW MFMAs instead of all
+    // conversion running before the stage's first MFMA.  INT4 sums each
+    // group (this stage) apart in g and applies the group scale at the end.
+    floatx4 g[MTW][NTW];
 #pragma unroll
-    for (int mt = 0; mt < MTW; mt++) {
-      floatx4 g[NTW];
+    for (int i = 0; i < 4; i++) {
+      half8_t bw[NTW];
 #pragma unroll
-      for (int t = 0; t < NTW; t++) g[t] = BITS == 4 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : acc[mt][t];
+      for (int t = 0; t < NTW; t++) {
+        if constexpr (BITS == 4) bw[t] = int4x8_to_half8(wr[t][0][i]);
+        else bw[t] = int8x8_to_half8(wr[t][i >> 1][2 * (i & 1)], wr[t][i >> 1][2 * (i & 1) + 1]);
+      }
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
+      for (int mt = 0; mt < MTW; mt++) {
         const int phys = (mt * 16 + c) * 16 + ((i * 4 + qd) ^ c);
         const half8_t ah = la[phys], al = la[PLANE + phys];
 #pragma unroll
-        for (int t = 0; t < NTW; t++) g[t] = mfma16x16x32(ah, bw[i][t], g[t]);
+        for (int t = 0; t < NTW; t++) {
+          const floatx4 g0 = i > 0 ? g[mt][t] : (BITS == 4 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : acc[mt][t]);
+          g[mt][t] = mfma16x16x32(ah, bw[t], g0);
+        }
 #pragma unroll
-        for (int t = 0; t < NTW; t++) g[t] = mfma16x16x32(al, bw[i][t], g[t]);
+        for (int t = 0; t < NTW; t++) g[mt][t] = mfma16x16x32(al, bw[t], g[mt][t]);
       }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
       for (int t = 0; t < NTW; t++) {
         if constexpr (BITS == 4) {
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[mt][t][i] = __builtin_fmaf(sf[t], g[t][i], acc[mt][t][i]);
+          for (int i = 0; i < 4; i++) acc[mt][t][i] = __builtin_fmaf(sf[t], g[mt][t][i], acc[mt][t][i]);
         } else {
-          acc[mt][t] = g[t];
+          acc[mt][t] = g[mt][t];
         }
       }
-    }
   }
 
 #pragma unroll
@@ -1096,6 +1122,8 @@ struct Plan {
   int64_t nstages = 0;  // gemm: 128-column K stages
   int64_t spz = 0;      // gemm: stages per K split
   int64_t splits = 1;   // gemm: K splits (partials + ordered reduction when > 1)
+  int gm = 1;           // gemm: m-tiles per band of the workgroup order
+  int wsnc = 0;         // gemm: consumer waves of the warp-specialized kernel
   int64_t mpad = 0;     // gemm: operand-plane rows (M rounded up to the row tile)
   bool wspec = false;   // gemm: warp-specialized DMA kernel (prefill chunks)
   int64_t pitch = 0;    // skinny: entries per (quad, A-row) in the lane-major layout
@@ -1182,7 +1210,12 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   p.wspec = m >= kGemmWsMinM;
   p.mtw = (m <= 32 && !p.wspec) ? 2 : 4;
   p.tiles_m = (m + 16 * p.mtw - 1) / (16 * p.mtw);
-  p.tiles_n = (n + kGemmBN - 1) / kGemmBN;
+  if (p.wspec) {
+    const int64_t wide = (n + 64 * kWsWideNC - 1) / (64 * kWsWideNC);
+    p.wsnc = bits == 4 && p.tiles_m * wide >= kWsWideMinTiles ? kWsWideNC : kWsNC;
+  }
+  const int64_t bn = p.wspec ? 64 * p.wsnc : kGemmBN;
+  p.tiles_n = (n + bn - 1) / bn;
   p.nstages = keff / 128;
   // Split K only as far as needed to give every CU two workgroups.
   const int64_t tiles = p.tiles_m * p.tiles_n;
@@ -1193,6 +1226,12 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
   p.spz = (p.nstages + s - 1) / s;
   p.splits = (p.nstages + p.spz - 1) / p.spz;
   p.mpad = p.tiles_m * 16 * p.mtw;
+  // Bands of m-tiles whose operand planes (BM rows x K x 4 bytes each) fit
+  // about 2 MiB of an XCD's L2.
+  {
+    const int64_t per_mtile = 16 * p.mtw * keff * 4;
+    p.gm = (int)std::max<int64_t>(1, std::min<int64_t>(p.tiles_m, (2 << 20) / per_mtile));
+  }
   // Operand planes (2 x 16 bytes per entry), then split-K partials.
   p.ws = (size_t)(2 * 16 * p.nstages * p.mpad * 16) +
          (p.splits > 1 ? (size_t)(4 * p.splits * m * n) : 0);
@@ -1300,7 +1339,7 @@ void launch_gemm_t(const Plan& p, const half8_t* planes, int64_t m, const uint8_
   const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
   gemm_kernel<BITS, MTW, kGemmNTW, kGemmWN><<<blocks, 64 * kGemmWN, 0, st>>>(
       planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m, (int)p.tiles_n,
-      bias, y, ldy, n, part);
+      p.gm, bias, y, ldy, n, part);
 }
 
 template <int BITS>
@@ -1315,9 +1354,17 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
   float* part = p.splits > 1 ? reinterpret_cast<float*>(planes + 2 * entries) : nullptr;
   if (p.wspec) {
     const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
-    gemm_ws_kernel<BITS, BITS == 4 ? 3 : 2><<<blocks, kWsThreads, 0, st>>>(
-        planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m,
-        (int)p.tiles_n, bias, y, ldy, n, part);
+#define KQ_WS(D_, NC_)                                                                          \
+  gemm_ws_kernel<BITS, D_, NC_><<<blocks, 64 * (NC_ + 1), 0, st>>>(                            \
+      planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m,               \
+      (int)p.tiles_n, p.gm, bias, y, ldy, n, part)
+    if constexpr (BITS == 4) {
+      if (p.wsnc == kWsWideNC) KQ_WS(2, kWsWideNC);
+      else KQ_WS(3, kWsNC);
+    } else {
+      KQ_WS(2, kWsNC);
+    }
+#undef KQ_WS
   } else if (p.mtw == 2) {
     launch_gemm_t<BITS, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   } else {

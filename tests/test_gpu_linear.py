@@ -132,6 +132,13 @@ def test_gemm_prefill_kernel_edges(gpu, m, n, k, scheme):
     _run(gpu, m, n, k, scheme, seed=m + n)
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 14400, 512), (300, 28700, 256)])
+def test_gemm_wide_consumer_tiles(gpu, m, n, k):
+    """INT4 grids that fill the GPU without a K split run 7 consumer waves
+    (448-column tiles): last column tile partial, last row tile partial."""
+    _run(gpu, m, n, k, "int4", seed=m + k)
+
+
 @pytest.mark.parametrize("m,n,k,g,scheme", [(16, 512, 512, 32, "int4"), (3, 512, 512, 256, "int4"),
                                             (40, 96, 500, 128, "int4"), (4, 70, 100, 128, "int8"),
                                             (33, 70, 100, 64, "int4"), (2, 16, 1, 128, "int4"),
