@@ -124,6 +124,32 @@ int kq_linear_argmax_int4(const float* x, int64_t m, int64_t ldx, const uint8_t*
                           int64_t* tokens, void* workspace, size_t workspace_bytes,
                           kq_stream_t stream);
 
+/* Workspace bytes for kq_linear_silu_mul_int8 / _int4 with these sizes
+ * (host only; nh = gate / up out_features). */
+size_t kq_linear_silu_mul_workspace_bytes(int scheme, int64_t m, int64_t nh, int64_t k,
+                                          int64_t group_size);
+
+/* The MLP input of the decoder layer (engine/model.py:147 runs layer.mlp, the
+ * HF MLP down_proj(act_fn(gate_proj(x)) * up_proj(x)) whose gate_proj and
+ * up_proj are QuantizedLinear after engine/model.py:80-91):
+ * act[m, j] = silu(g) * u with g, u the kq_linear_int8 sums of gate row j and
+ * up row j (silu(v) = v / (1 + exp(-v))).  payload / scales / bias hold the
+ * two weights interleaved by 16-row tiles (rows 32 b .. 32 b + 15: gate rows
+ * 16 b .., the next 16: the same up rows; 2 nh rows); nh % 16 == 0.
+ * act: [m, nh] (ldact).  workspace: at least
+ * kq_linear_silu_mul_workspace_bytes(8, ...) bytes. */
+int kq_linear_silu_mul_int8(const float* x, int64_t m, int64_t ldx, const int8_t* payload,
+                            const uint16_t* scales, const float* bias, float* act,
+                            int64_t ldact, int64_t nh, int64_t k, void* workspace,
+                            size_t workspace_bytes, kq_stream_t stream);
+
+/* As kq_linear_silu_mul_int8 over interleaved INT4 payload and group scales
+ * (the projections of kq_linear_int4; engine/model.py:147). */
+int kq_linear_silu_mul_int4(const float* x, int64_t m, int64_t ldx, const uint8_t* payload,
+                            const uint16_t* scales, int64_t group_size, int64_t k_padded,
+                            const float* bias, float* act, int64_t ldact, int64_t nh, int64_t k,
+                            void* workspace, size_t workspace_bytes, kq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -198,7 +198,7 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     const uint8_t* wq, const uint16_t* sc, int64_t row_bytes,
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
     const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
-    int2* __restrict__ argp) {
+    int2* __restrict__ argp, int pairs) {
   static_assert(!M1 || (A_LDS && HL && !REM), "single-row instances stage in LDS, pre-loads only");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int TPU = BITS == 4 ? 4 : 2;  // k-steps per unit
@@ -442,6 +442,32 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 #pragma unroll
     for (int i = 0; i < 4; i++) red[((wave * NT + t) * 16 + 4 * qd + i) * 16 + c] = acc[t][i];
   __syncthreads();
+  // Gate / up pairs (NT == 2, weights interleaved by 16-row tiles): tile 0
+  // holds gate rows, tile 1 the up rows of the same 16 output columns;
+  // y[m][16 b + c] = silu(g) * up.
+  if constexpr (NT == 2) {
+    if (pairs) {
+      for (int o = tid; o < M * 16; o += blockDim.x) {
+        const int m = o >> 4, cc = o & 15;
+        const int64_t ngate = ncol0 + cc, nup = ngate + 16;
+        if (nup < N) {
+          float g = 0.0f, u = 0.0f;
+          for (int w = 0; w < nwaves; w++) {
+            g += red[((w * NT) * 16 + m) * 16 + cc];
+            u += red[((w * NT + 1) * 16 + m) * 16 + cc];
+            if constexpr (HL) {
+              g += red[((w * NT) * 16 + m + 8) * 16 + cc];
+              u += red[((w * NT + 1) * 16 + m + 8) * 16 + cc];
+            }
+          }
+          if constexpr (BITS == 8) { g *= f16_bits_to_f32(sc[ngate]); u *= f16_bits_to_f32(sc[nup]); }
+          if (bias) { g += bias[ngate]; u += bias[nup]; }
+          y[m * ldy + (int64_t)blockIdx.x * 16 + cc] = g / (1.0f + expf(-g)) * u;
+        }
+      }
+      return;
+    }
+  }
   // y may be null (greedy argmax only).  With argp, the 16 lanes of a row's
   // tile reduce their (logit, column) pairs and lane 0 writes the tile's
   // partial: argp[m * tiles + tile].
@@ -1124,13 +1150,16 @@ struct Plan {
   int64_t splits = 1;   // gemm: K splits (partials + ordered reduction when > 1)
   int gm = 1;           // gemm: m-tiles per band of the workgroup order
   int wsnc = 0;         // gemm: consumer waves of the warp-specialized kernel
+  bool pairs = false;   // skinny: gate / up tile pairs, silu(gate) * up epilogue
   int64_t mpad = 0;     // gemm: operand-plane rows (M rounded up to the row tile)
   bool wspec = false;   // gemm: warp-specialized DMA kernel (prefill chunks)
   int64_t pitch = 0;    // skinny: entries per (quad, A-row) in the lane-major layout
   size_t ws = 0;        // workspace bytes
 };
 
-Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp) {
+// pairs: N rows interleave gate and up weights by 16-row tiles; a skinny
+// plan then takes exactly two tiles per wave (one gate / up pair).
+Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp, bool pairs = false) {
   Plan p;
   const bool tiled = bits == 4 ? (g == 128) : (k % 64 == 0);
   if (!tiled) { p.path = Path::Generic; return p; }
@@ -1151,6 +1180,10 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp)
     if (m >= kSkinnyNTMinM) {
       const int64_t t16 = (n + 15) / 16;
       p.nt = t16 / 4 >= kSkinnyMinGroups ? 4 : (t16 / 2 >= kSkinnyMinGroups ? 2 : 1);
+    }
+    if (pairs) {
+      p.nt = 2;
+      p.pairs = true;
     }
     const int64_t ntiles = (n + 16 * p.nt - 1) / (16 * p.nt);
     auto waves_for = [&](int64_t pw) { return ntiles * ((p.nunits + pw - 1) / pw); };
@@ -1248,10 +1281,11 @@ void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStrea
                       const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                       const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n,
                       int2* argp) {
+  const int pairs = p.pairs ? 1 : 0;
 #define KQ_SKINNY(KS_, NT_)                                                                   \
   skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC, M1, REM><<<grid, block, shm, st>>>(            \
       x, ldx, (int)m, k, xvec, wq, sc, row_bytes, ng, p.nunits, p.per_wave, (int)p.pitch, xa, \
-      bias, y, ldy, n, argp)
+      bias, y, ldy, n, argp, pairs)
   if (p.nt == 4) {
     if (p.ks == 2) KQ_SKINNY(2, 4); else KQ_SKINNY(4, 4);
   } else if (p.nt == 2) {
@@ -1539,4 +1573,97 @@ extern "C" int kq_linear_argmax_int4(const float* x, int64_t m, int64_t ldx, con
   const Plan p = make_plan(4, m, n, k, g, kp);
   return linear_argmax<4>(p, x, m, ldx, payload, scales, kp / 2, g, kp / g, bias, logits, ldl, n, k,
                           tokens, ws, ws_bytes, kq_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Fused gate / up projection with the SiLU gate: act = silu(x Wg^T + bg) *
+// (x Wu^T + bu), the MLP input of HF Llama / Qwen2 (down_proj(act_fn(
+// gate_proj(x)) * up_proj(x))), which Kshipra runs inside layer.mlp
+// (engine/model.py:147) as two QuantizedLinear calls and two elementwise ops.  The packed
+// weight (and scales, bias) interleave the two by 16-row tiles: rows
+// 32 b .. 32 b + 15 are gate rows 16 b .. 16 b + 15, the next 16 the same up
+// rows.  Skinny path: one gate / up tile pair per wave, silu * up in the
+// epilogue.  Other paths: the interleaved product goes to the workspace and
+// silu_mul_pairs_kernel combines it.
+// ---------------------------------------------------------------------------
+namespace {
+
+__global__ __launch_bounds__(256) void silu_mul_pairs_kernel(const float* __restrict__ yi, int64_t m,
+                                                             int64_t nh, float* __restrict__ act,
+                                                             int64_t lda) {
+  const int64_t total = m * nh;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / nh, j = e - r * nh;
+    const int64_t src = r * 2 * nh + (j >> 4) * 32 + (j & 15);
+    const float g = yi[src], u = yi[src + 16];
+    act[r * lda + j] = g / (1.0f + expf(-g)) * u;
+  }
+}
+
+size_t silu_mul_ws(const Plan& p, int64_t m, int64_t nh) {
+  return p.path == Path::Skinny ? p.ws : align256(p.ws) + (size_t)(m * 2 * nh) * sizeof(float);
+}
+
+int check_silu_args(const float* x, int64_t m, int64_t ldx, const void* wq, const void* sc,
+                    const float* act, int64_t lda, int64_t nh, int64_t k) {
+  KQ_REQUIRE(x != nullptr && wq != nullptr && sc != nullptr && act != nullptr, "null pointer argument");
+  KQ_REQUIRE(m > 0 && nh > 0 && k > 0, "empty linear");
+  KQ_REQUIRE(nh % 16 == 0, "gate / up out_features must be a multiple of 16 (16-row tile pairs)");
+  KQ_REQUIRE(ldx >= k, "ldx smaller than in_features");
+  KQ_REQUIRE(lda >= nh, "ldact smaller than out_features");
+  return KQ_OK;
+}
+
+template <int BITS>
+int linear_silu_mul(const Plan& p, const float* x, int64_t m, int64_t ldx, const uint8_t* wq,
+                    const uint16_t* sc, int64_t row_bytes, int64_t g, int64_t ng, const float* bias,
+                    float* act, int64_t lda, int64_t nh, int64_t k, void* ws, size_t ws_bytes,
+                    hipStream_t st) {
+  if (ws_bytes < silu_mul_ws(p, m, nh) || (silu_mul_ws(p, m, nh) > 0 && ws == nullptr))
+    return kq_set_error(KQ_ERR_WORKSPACE, "workspace missing or smaller than kq_linear_silu_mul_workspace_bytes()");
+  const int64_t n = 2 * nh;
+  if (p.path == Path::Skinny)
+    return launch_skinny<BITS>(p, x, ldx, m, k, wq, sc, row_bytes, ng, bias, act, lda, n, ws, st);
+  float* yi = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(p.ws));
+  int s;
+  if (p.path == Path::Gemm) s = launch_gemm<BITS>(p, x, ldx, m, k, wq, sc, row_bytes, ng, bias, yi, n, n, ws, st);
+  else s = launch_generic<BITS>(x, ldx, m, wq, sc, row_bytes, g, ng, bias, yi, n, n, k, st);
+  if (s != KQ_OK) return s;
+  const unsigned blocks = (unsigned)std::min<int64_t>((m * nh + 255) / 256, 8192);
+  silu_mul_pairs_kernel<<<blocks, 256, 0, st>>>(yi, m, nh, act, lda);
+  return kq_check_launch(BITS == 4 ? "kq_linear_silu_mul_int4" : "kq_linear_silu_mul_int8");
+}
+
+}  // namespace
+
+extern "C" size_t kq_linear_silu_mul_workspace_bytes(int scheme, int64_t m, int64_t nh, int64_t k,
+                                                     int64_t group_size) {
+  if (m <= 0 || nh <= 0 || k <= 0) return 0;
+  if (scheme == 8) return silu_mul_ws(make_plan(8, m, 2 * nh, k, 0, k, true), m, nh);
+  if (group_size <= 0) return 0;
+  const int64_t kp = (k + group_size - 1) / group_size * group_size;
+  return silu_mul_ws(make_plan(4, m, 2 * nh, k, group_size, kp, true), m, nh);
+}
+
+extern "C" int kq_linear_silu_mul_int8(const float* x, int64_t m, int64_t ldx, const int8_t* payload,
+                                       const uint16_t* scales, const float* bias, float* act,
+                                       int64_t ldact, int64_t nh, int64_t k, void* ws,
+                                       size_t ws_bytes, kq_stream_t stream) {
+  if (int s = check_silu_args(x, m, ldx, payload, scales, act, ldact, nh, k)) return s;
+  const Plan p = make_plan(8, m, 2 * nh, k, 0, k, true);
+  return linear_silu_mul<8>(p, x, m, ldx, reinterpret_cast<const uint8_t*>(payload), scales, k, 1, 1,
+                            bias, act, ldact, nh, k, ws, ws_bytes, kq_stream(stream));
+}
+
+extern "C" int kq_linear_silu_mul_int4(const float* x, int64_t m, int64_t ldx, const uint8_t* payload,
+                                       const uint16_t* scales, int64_t g, int64_t kp,
+                                       const float* bias, float* act, int64_t ldact, int64_t nh,
+                                       int64_t k, void* ws, size_t ws_bytes, kq_stream_t stream) {
+  if (int s = check_silu_args(x, m, ldx, payload, scales, act, ldact, nh, k)) return s;
+  KQ_REQUIRE(g > 0 && g % 2 == 0, "group_size must be a positive even integer");
+  KQ_REQUIRE(kp % g == 0 && kp >= k && kp - k < g, "inconsistent in_features_padded");
+  const Plan p = make_plan(4, m, 2 * nh, k, g, kp, true);
+  return linear_silu_mul<4>(p, x, m, ldx, payload, scales, kp / 2, g, kp / g, bias, act, ldact, nh, k,
+                            ws, ws_bytes, kq_stream(stream));
 }

@@ -13,8 +13,10 @@ decoder that runs every projection through ``QuantizedLinear`` on the GPU.
   length), then M = 1 decode steps, first-index argmax.  The seven projections
   of each layer are ``QuantizedLinear`` modules (the hot path); RMSNorm, RoPE,
   attention over a contiguous KV cache and the fp32 lm_head are plain torch
-  ops on the same device and stream.  With ``fuse=True`` q/k/v and gate/up run
-  as one ``FusedQuantizedLinear`` launch each (same weights, row-stacked).
+  ops on the same device and stream.  With ``fuse=True`` q/k/v run as one
+  ``FusedQuantizedLinear`` launch (same weights, row-stacked) and gate/up with
+  the SiLU gate as one ``FusedGateUpSiLU`` launch (intermediate size a
+  multiple of 16; else a ``FusedQuantizedLinear`` and torch's silu * up).
   ``lm_head_scheme="int8"|"int4"`` quantizes the vocab projection too (the
   reference keeps it fp32) and takes each greedy token from the argmax fused
   into that projection.
@@ -35,7 +37,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .quantization import (FusedQuantizedLinear, QuantizedLinear, QuantizedWeight,
+from .quantization import (FusedGateUpSiLU, FusedQuantizedLinear, QuantizedLinear, QuantizedWeight,
                            quantize_int4_per_group, quantize_int8_per_channel, quantized_linear,
                            quantized_linear_argmax)
 
@@ -141,7 +143,11 @@ class DecoderLM:
                 del lin
             if fuse:
                 layer["qkv"] = FusedQuantizedLinear([layer.pop(p) for p in ("q_proj", "k_proj", "v_proj")])
-                layer["gate_up"] = FusedQuantizedLinear([layer.pop(p) for p in ("gate_proj", "up_proj")])
+                gate, up = layer.pop("gate_proj"), layer.pop("up_proj")
+                if gate.out_features % 16 == 0:
+                    layer["gate_up_act"] = FusedGateUpSiLU(gate, up)
+                else:
+                    layer["gate_up"] = FusedQuantizedLinear([gate, up])
             self.layers.append(layer)
         exps = torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim
         self.inv_freq = (1.0 / (cfg.rope_theta ** exps)).to(device)
@@ -216,11 +222,14 @@ class DecoderLM:
             h = res + layer["o_proj"](a.contiguous())
             res = h
             x = _rms_norm(h, layer["post_norm"], c.rms_norm_eps)
-            if "gate_up" in layer:
-                gate, up = layer["gate_up"](x)
+            if "gate_up_act" in layer:
+                act = layer["gate_up_act"](x)
             else:
-                gate, up = layer["gate_proj"](x), layer["up_proj"](x)
-            act = F.silu(gate) * up
+                if "gate_up" in layer:
+                    gate, up = layer["gate_up"](x)
+                else:
+                    gate, up = layer["gate_proj"](x), layer["up_proj"](x)
+                act = F.silu(gate) * up
             h = res + layer["down_proj"](act)
         self.pos = S
         return _rms_norm(h, self.norm, c.rms_norm_eps)

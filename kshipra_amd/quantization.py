@@ -59,6 +59,9 @@ __all__ = [
     "concat_quantized",
     "FusedQuantizedLinear",
     "quantized_linear_argmax",
+    "interleave_gate_up",
+    "quantized_gate_up_silu",
+    "FusedGateUpSiLU",
 ]
 
 
@@ -506,4 +509,126 @@ class FusedQuantizedLinear(nn.Module):
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.splits}, "
+                f"scheme={self.scheme}, storage_bytes={self.weight.storage_bytes()}")
+
+
+# ---------------------------------------------------------------------- #
+# Gate / up projection with the SiLU gate (the MLP input)
+# ---------------------------------------------------------------------- #
+
+_PAIR = 16  # rows per tile of the gate / up interleave
+
+
+def _interleave_rows(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    n = g.shape[0]
+    rest = g.shape[1:]
+    return torch.stack([g.reshape(n // _PAIR, _PAIR, *rest), u.reshape(n // _PAIR, _PAIR, *rest)],
+                       dim=1).reshape(2 * n, *rest)
+
+
+def interleave_gate_up(gate: QuantizedWeight, up: QuantizedWeight) -> QuantizedWeight:
+    """Gate and up weights interleaved by 16-row tiles (rows 32 b .. 32 b + 15
+    are gate rows 16 b .., the next 16 the same up rows), the layout the fused
+    SiLU-gated projection reads.  Rows are quantized independently
+    (engine/quantization.py:206-208, :293-295), so this is a permutation of
+    the row-stacked quantization, bit for bit."""
+    if (gate.scheme != up.scheme or gate.original_shape != up.original_shape
+            or gate.group_size != up.group_size
+            or gate.in_features_padded != up.in_features_padded):
+        raise QuantizationError("gate and up differ in scheme, shape or group size")
+    if gate.payload.device != up.payload.device:
+        raise QuantizationError("gate and up live on different devices")
+    n, k = gate.original_shape
+    if n % _PAIR != 0:
+        raise QuantizationError(f"out_features {n} is not a multiple of {_PAIR}")
+    return QuantizedWeight(
+        payload=_interleave_rows(gate.payload, up.payload),
+        scales=_interleave_rows(gate.scales, up.scales),
+        scheme=gate.scheme, original_shape=(2 * n, k), group_size=gate.group_size,
+        in_features_padded=gate.in_features_padded)
+
+
+def quantized_gate_up_silu(x: torch.Tensor, qw: QuantizedWeight,
+                           bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``silu(x Wg^T + bg) * (x Wu^T + bu)`` -- the input of the MLP's down
+    projection (engine/model.py:147 runs ``layer.mlp``, whose gate_proj and
+    up_proj are ``QuantizedLinear`` after engine/model.py:80-91) -- from the
+    interleaved weight of ``interleave_gate_up`` (and bias interleaved the
+    same way), in one dequant-matmul launch whose epilogue applies the gate
+    (M <= 16), or the matmul plus one pairing kernel."""
+    _lib.require_device(x, "input")
+    rows, in_features = qw.original_shape
+    nh = rows // 2
+    if x.shape[-1] != in_features:
+        raise RuntimeError(
+            f"mat1 and mat2 shapes cannot be multiplied "
+            f"({x.numel() // max(x.shape[-1], 1)}x{x.shape[-1]} and {in_features}x{rows})")
+    if x.device != qw.payload.device:
+        raise RuntimeError(f"input on {x.device} but weight on {qw.payload.device}")
+    lib = _lib.load()
+    out_dtype = x.dtype
+    x2 = x.reshape(-1, in_features)
+    if x2.dtype != torch.float32:
+        x2 = x2.to(torch.float32)
+    if x2.stride(1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < in_features):
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    act = torch.empty((m, nh), dtype=torch.float32, device=x.device)
+    if m > 0:
+        b = None
+        if bias is not None:
+            b = bias.detach()
+            if b.dtype != torch.float32 or not b.is_contiguous():
+                b = b.to(torch.float32).contiguous()
+        ldx = x2.stride(0) if m > 1 else in_features
+        stream = _lib.stream_of(x2)
+        if qw.scheme == "int8_per_channel":
+            nbytes = lib.kq_linear_silu_mul_workspace_bytes(8, m, nh, in_features, 0)
+            ws = _lib.workspace(x.device, stream, nbytes)
+            _lib.check(lib.kq_linear_silu_mul_int8(
+                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), _lib.ptr(b),
+                act.data_ptr(), nh, nh, in_features, _lib.ptr(ws), nbytes, stream))
+        else:
+            g = qw.group_size
+            nbytes = lib.kq_linear_silu_mul_workspace_bytes(4, m, nh, in_features, g)
+            ws = _lib.workspace(x.device, stream, nbytes)
+            _lib.check(lib.kq_linear_silu_mul_int4(
+                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), g,
+                qw.in_features_padded, _lib.ptr(b), act.data_ptr(), nh, nh, in_features,
+                _lib.ptr(ws), nbytes, stream))
+    act = act.reshape(*x.shape[:-1], nh)
+    return act if out_dtype == torch.float32 else act.to(out_dtype)
+
+
+class FusedGateUpSiLU(nn.Module):
+    """``silu(gate(x)) * up(x)`` for two ``QuantizedLinear`` of one input (the
+    Llama / Qwen2 MLP's gate_proj and up_proj) as one launch over their
+    16-row-tile interleaved weight.  Same values as the two projections
+    followed by ``F.silu(g) * u``, up to fp32 summation order and the
+    exponential's rounding."""
+
+    def __init__(self, gate: "QuantizedLinear", up: "QuantizedLinear") -> None:
+        super().__init__()
+        for p in (gate, up):
+            if not isinstance(p, QuantizedLinear):
+                raise QuantizationError(f"expected QuantizedLinear, got {type(p).__name__}")
+        self.in_features = gate.in_features
+        self.out_features = gate.out_features
+        self.scheme = gate.scheme
+        self.weight = interleave_gate_up(gate.weight, up.weight)
+        if gate.bias is not None or up.bias is not None:
+            dev = self.weight.payload.device
+
+            def _b(p):
+                return (p.bias.detach().to(torch.float32) if p.bias is not None
+                        else torch.zeros(p.out_features, dtype=torch.float32, device=dev))
+            self.register_buffer("bias", _interleave_rows(_b(gate), _b(up)))
+        else:
+            self.bias = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return quantized_gate_up_silu(x, self.weight, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"scheme={self.scheme}, storage_bytes={self.weight.storage_bytes()}")

@@ -187,7 +187,8 @@ def test_header_cites_reference_for_every_compute_entry_point():
                  "kq_linear_int8", "kq_linear_int4", "kq_check_finite"):
         block = text[:text.index(name + "(")].rsplit("/*", 1)[-1]
         assert "engine/quantization.py" in block, name
-    for name in ("kq_linear_argmax_int8", "kq_linear_argmax_int4"):
+    for name in ("kq_linear_argmax_int8", "kq_linear_argmax_int4",
+                 "kq_linear_silu_mul_int8", "kq_linear_silu_mul_int4"):
         block = text[:text.index(name + "(")].rsplit("/*", 1)[-1]
         assert "engine/model.py" in block, name
 
@@ -232,3 +233,51 @@ def test_concat_rejects_mismatched_parts():
     with pytest.raises(QuantizationError):
         from kshipra_amd.quantization import FusedQuantizedLinear
         FusedQuantizedLinear([nn.Linear(4, 4)])
+
+
+@pytest.mark.parametrize("scheme", ["int8", "int4"])
+def test_gate_up_interleave_is_a_row_permutation(scheme):
+    """interleave_gate_up equals quantizing the fp32 weight whose rows are the
+    gate / up rows interleaved by 16-row tiles, bit for bit."""
+    import numpy as np
+    from cases import gaussian
+    from kshipra_amd.quantization import interleave_gate_up
+    g, u = gaussian((48, 300), seed=80), gaussian((48, 300), seed=81)
+    fused = interleave_gate_up(_oracle_qw(g, scheme), _oracle_qw(u, scheme))
+    rows = np.concatenate([np.concatenate([g[16 * b:16 * b + 16], u[16 * b:16 * b + 16]])
+                           for b in range(3)])
+    whole = _oracle_qw(rows, scheme)
+    assert fused.original_shape == (96, 300)
+    assert torch.equal(fused.payload, whole.payload)
+    assert torch.equal(fused.scales.view(torch.int16), whole.scales.view(torch.int16))
+
+
+def test_gate_up_interleave_rejects():
+    from cases import gaussian
+    from kshipra_amd.quantization import FusedGateUpSiLU, interleave_gate_up
+    a = _oracle_qw(gaussian((32, 256), seed=1), "int4")
+    for bad in (_oracle_qw(gaussian((32, 384), seed=2), "int4"),   # in_features
+                _oracle_qw(gaussian((48, 256), seed=3), "int4"),   # out_features
+                _oracle_qw(gaussian((32, 256), seed=4), "int8")):  # scheme
+        with pytest.raises(QuantizationError):
+            interleave_gate_up(a, bad)
+    odd = _oracle_qw(gaussian((24, 256), seed=5), "int4")           # not 16-row tiles
+    with pytest.raises(QuantizationError):
+        interleave_gate_up(odd, odd)
+    with pytest.raises(QuantizationError):
+        FusedGateUpSiLU(nn.Linear(4, 4), nn.Linear(4, 4))
+
+
+def test_silu_mul_workspace_and_argument_errors():
+    lib = _lib.load()
+    # M = 1 gate / up of Llama-3-8B: pairs of tiles in LDS, no workspace
+    assert lib.kq_linear_silu_mul_workspace_bytes(4, 1, 14336, 4096, 128) == 0
+    # GEMM path: operand planes (64-row tile) + the interleaved product
+    ws = lib.kq_linear_silu_mul_workspace_bytes(4, 64, 14336, 4096, 128)
+    assert ws >= 4 * 64 * 4096 + 4 * 64 * 2 * 14336
+    # out_features not a multiple of 16, ldact too small, null act
+    assert lib.kq_linear_silu_mul_int8(1, 1, 64, 1, 1, None, 1, 24, 24, 64, None, 0, None) == _lib.KQ_ERR_ARG
+    assert lib.kq_linear_silu_mul_int8(1, 1, 64, 1, 1, None, 1, 16, 32, 64, None, 0, None) == _lib.KQ_ERR_ARG
+    assert lib.kq_linear_silu_mul_int4(1, 1, 128, 1, 1, 128, 128, None, None, 32, 32, 128, None, 0,
+                                       None) == _lib.KQ_ERR_ARG
+    assert lib.kq_last_error() not in (None, b"")
