@@ -150,6 +150,50 @@ int kq_linear_silu_mul_int4(const float* x, int64_t m, int64_t ldx, const uint8_
                             const float* bias, float* act, int64_t ldact, int64_t nh, int64_t k,
                             void* workspace, size_t workspace_bytes, kq_stream_t stream);
 
+/* ---- Paged K/V pool and chunked attention (fp32) -------------------------
+ * Pool element (block, head, offset, d) of one layer's K (or V) half is at
+ * pool[block * pool_ld_blk + head * pool_ld_head + offset * pool_ld_off + d]
+ * (d contiguous): for Kshipra's pool [num_blocks, layers, 2, H_kv, B, D] the
+ * layer-i K half pool[:, i, 0] has strides (layers*2*H_kv*B*D, B*D, D).
+ * Pointers 16-byte aligned, strides multiples of 4 elements. */
+
+/* Replaces the K/V store loop of KshipraModel.forward, engine/model.py:124-129:
+ * for every t < tokens with 0 <= slot_mapping[t] < num_blocks * block_size,
+ * K / V element (t, head, d) -- k[t * src_ld_tok + head * src_ld_head + d] --
+ * goes to (slot / block_size, head, slot % block_size, d) of k_pool / v_pool.
+ * Negative slots are skipped; non-negative slots must be distinct (the Python
+ * mirror keeps the last writer of a repeated slot, as the reference loop does,
+ * by passing -1 for the earlier ones).  slot_mapping: device int64 [tokens]. */
+int kq_paged_kv_write_f32(const float* k, const float* v, int64_t tokens, int64_t kv_heads,
+                          int64_t head_dim, int64_t src_ld_tok, int64_t src_ld_head,
+                          const int64_t* slot_mapping, float* k_pool, float* v_pool,
+                          int64_t num_blocks, int64_t block_size, int64_t pool_ld_blk,
+                          int64_t pool_ld_head, int64_t pool_ld_off, kq_stream_t stream);
+
+/* Workspace of kq_chunked_attention_f32 in bytes (0: none needed; 0 also for
+ * invalid shapes, which the entry point then rejects). */
+size_t kq_chunked_attention_workspace_bytes(int64_t q_heads, int64_t kv_heads, int64_t chunk_len,
+                                            int64_t head_dim, int64_t prefix_len);
+
+/* Replaces chunked_attention, engine/chunked_prefill.py:93-140.
+ * q element (h, i, d) at q[h * q_ld_head + i * q_ld_tok + d], h < q_heads,
+ * i < chunk_len; out likewise (out_ld_head, out_ld_tok).  Query i sits at
+ * position prefix_len + i and attends, with scale 1/sqrt(head_dim) and the
+ * online softmax, to keys 0 .. prefix_len + i of KV head h / (q_heads /
+ * kv_heads); key position p lives in block block_table[p / block_size] at
+ * offset p % block_size.  head_dim 64 or 128; q_heads % kv_heads == 0;
+ * table_len >= ceil((prefix_len + chunk_len) / block_size); block_table is
+ * device int32, entries in [0, num_blocks) (an entry outside is read as block
+ * num_blocks - 1: memory-safe, result unspecified).  fp32 throughout. */
+int kq_chunked_attention_f32(const float* q, int64_t q_heads, int64_t chunk_len, int64_t head_dim,
+                             int64_t q_ld_head, int64_t q_ld_tok, const float* k_pool,
+                             const float* v_pool, int64_t kv_heads, int64_t num_blocks,
+                             int64_t block_size, int64_t pool_ld_blk, int64_t pool_ld_head,
+                             int64_t pool_ld_off, const int32_t* block_table, int64_t table_len,
+                             int64_t prefix_len, float* out, int64_t out_ld_head,
+                             int64_t out_ld_tok, void* workspace, size_t workspace_bytes,
+                             kq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

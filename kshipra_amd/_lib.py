@@ -18,7 +18,7 @@ from ._errors import QuantizationError
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkshipra_quant.so")
-ABI_VERSION = 102
+ABI_VERSION = 103
 
 KQ_OK, KQ_ERR_ARG, KQ_ERR_HIP, KQ_ERR_WORKSPACE = 0, 1, 2, 3
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
@@ -47,6 +47,12 @@ SIGNATURES = [
      [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     ("kq_linear_silu_mul_int4", _int,
      [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    ("kq_paged_kv_write_f32", _int,
+     [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    ("kq_chunked_attention_workspace_bytes", _sz, [_i64, _i64, _i64, _i64, _i64]),
+    ("kq_chunked_attention_f32", _int,
+     [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
+      _i64, _vp, _i64, _i64, _vp, _sz, _vp]),
 ]
 
 _lib = None

@@ -1,0 +1,422 @@
+// Paged K/V write and chunked (prefix + chunk) attention over the block pool,
+// fp32, for gfx950.
+//
+//  * kq_paged_kv_write_f32 -- the K/V store of KshipraModel.forward
+//    (engine/model.py:124-129): token t's K and V rows of every KV head go to
+//    pool[slot // B, layer, 0 / 1, :, slot % B, :], slot = slot_mapping[t].
+//    One thread moves 4 floats; HBM-bound, 2 x (read + write) per element.
+//  * kq_chunked_attention_f32 -- chunked_attention (engine/chunked_prefill.py:
+//    93-140): query i of the chunk (position prefix_len + i) attends to every
+//    key at position <= its own, read in place from the pool through the block
+//    table, with GQA (query head h reads KV head h / g) and the online softmax.
+//
+// Attention work decomposition.  Rows of one KV head are (query, head-in-group)
+// pairs, row = c * g + hh, so a 16-row tile spans 16 / g consecutive queries of
+// all g heads sharing the K / V stream.  One wave owns (KV head, 16-row tile,
+// key split) and walks its keys 16 at a time with fp32 MFMA 16x16x4:
+//
+//   S^T[key][row] = sum_d K[key][d] Q[row][d]          (D / 4 MFMAs)
+//   O^T[d][row]  += sum_key V[key][d] P[row][key]       (D / 4 MFMAs)
+//
+// Computing S^T (keys on the MFMA's row axis) leaves lane l holding row l % 16
+// and keys 4 (l / 16) + r in its 4 accumulators -- exactly the B operand
+// (P^T, k index l / 16) of the second product, so P never moves between
+// lanes.  Both reductions run in a permuted order chosen so every lane reads
+// contiguous memory: in the first product lane group q = l / 16 covers d in
+// [q D/4, (q+1) D/4) (D/16 float4 loads of its key's row), in the second lane
+// l % 16 = j covers d = (D/16) j + db, db = 0 .. D/16-1 (D/64 float4 loads per
+// key).  Row statistics (running max m, sum l) live in the lanes of their row;
+// one row's 16 scores are spread over lane groups, so the row max and sum take
+// two cross-lane steps.  Scores are in log2 units (Q is pre-scaled by
+// log2(e) / sqrt(D)) and exponentials are exp2.
+//
+// Splits: when KV heads x row tiles gives too few waves to fill the GPU
+// (decode, short chunks) the key range is split; each split writes its
+// unnormalised (m, l, acc) to the workspace and a second kernel merges them.
+#include <algorithm>
+#include <cmath>
+
+#include "kq_common.hpp"
+
+namespace {
+
+constexpr int kAttnWavesPerBlock = 4;
+constexpr int64_t kAttnTargetWaves = 2048;     // 8 waves per CU on 256 CUs
+constexpr int64_t kAttnMinTilesPerSplit = 4;   // >= 64 keys per split
+constexpr int64_t kAttnMaxSplits = 256;
+
+struct AttnArgs {
+  const float* q;
+  const float* kp;
+  const float* vp;
+  const int32_t* table;
+  float* out;
+  float* ws_acc;   // [splits][rows_total][D]
+  float* ws_ml;    // [splits][rows_total][2]
+  int64_t q_ld_head, q_ld_tok;
+  int64_t o_ld_head, o_ld_tok;
+  int64_t p_ld_blk, p_ld_head, p_ld_off;
+  int num_blocks, block_size;
+  int group, chunk, prefix, total;
+  int rowtiles, splits, split_keys, items, rows_total;
+  float qscale;
+};
+
+struct AttnPlan {
+  int64_t rowtiles, splits, split_keys, items;
+};
+
+AttnPlan attn_plan(int64_t hq, int64_t hkv, int64_t chunk, int64_t prefix) {
+  AttnPlan p{};
+  const int64_t g = hq / hkv;
+  p.rowtiles = (g * chunk + 15) / 16;
+  const int64_t ntiles = (prefix + chunk + 15) / 16;
+  const int64_t base = hkv * p.rowtiles;
+  int64_t splits = 1;
+  if (base < kAttnTargetWaves) {
+    splits = (kAttnTargetWaves + base - 1) / base;
+    splits = std::min(splits, (ntiles + kAttnMinTilesPerSplit - 1) / kAttnMinTilesPerSplit);
+    splits = std::min(std::max<int64_t>(splits, 1), kAttnMaxSplits);
+  }
+  const int64_t tiles_per_split = (ntiles + splits - 1) / splits;
+  p.splits = (ntiles + tiles_per_split - 1) / tiles_per_split;   // no empty tail split
+  p.split_keys = tiles_per_split * 16;
+  p.items = base * p.splits;
+  return p;
+}
+
+__device__ __forceinline__ floatx4 ld4(const float* p) {
+  return *reinterpret_cast<const floatx4*>(p);
+}
+
+// Pool row (block, head, offset) of key position pos, pos < total.
+__device__ __forceinline__ const float* key_row(const float* pool, const AttnArgs& a, int kvh,
+                                                int pos) {
+  const int j = pos / a.block_size;
+  unsigned blk = (unsigned)a.table[j];
+  blk = blk < (unsigned)a.num_blocks ? blk : (unsigned)(a.num_blocks - 1);
+  return pool + (int64_t)blk * a.p_ld_blk + (int64_t)kvh * a.p_ld_head +
+         (int64_t)(pos - j * a.block_size) * a.p_ld_off;
+}
+
+template <int D, bool BLK16>
+__global__ __launch_bounds__(64 * kAttnWavesPerBlock) void chunked_attention_kernel(const AttnArgs a) {
+  constexpr int DQ = D / 4;    // d per lane group in S^T = K Q^T
+  constexpr int DB = D / 16;   // d-blocks of O^T (floats per lane per key in V)
+  const int lane = threadIdx.x & 63;
+
+  // XCD-aware order: blocks b, b + 8, ... share an XCD (and its L2); give each
+  // XCD a contiguous range of items (same KV head, neighbouring row tiles).
+  int b = blockIdx.x;
+  if ((gridDim.x & 7) == 0) b = (b & 7) * (gridDim.x >> 3) + (b >> 3);
+  int item = b * kAttnWavesPerBlock + (threadIdx.x >> 6);
+  if (item >= a.items) return;
+  const int split = item % a.splits;
+  item /= a.splits;
+  const int rt = item % a.rowtiles;
+  const int kvh = item / a.rowtiles;
+
+  const int g = a.group;
+  const int rows = g * a.chunk;
+  const int j16 = lane & 15, grp = lane >> 4;
+  const int rho = rt * 16 + j16;
+  const bool rvalid = rho < rows;
+  const int c = rvalid ? rho / g : 0;
+  const int head = kvh * g + (rvalid ? rho - c * g : 0);
+  const int qpos = a.prefix + c;
+
+  float qv[DQ];
+  {
+    const float* qp = a.q + (int64_t)head * a.q_ld_head + (int64_t)c * a.q_ld_tok + DQ * grp;
+#pragma unroll
+    for (int i = 0; i < DQ / 4; ++i) {
+      floatx4 t = rvalid ? ld4(qp + 4 * i) : floatx4{0.f, 0.f, 0.f, 0.f};
+      qv[4 * i + 0] = t[0] * a.qscale;
+      qv[4 * i + 1] = t[1] * a.qscale;
+      qv[4 * i + 2] = t[2] * a.qscale;
+      qv[4 * i + 3] = t[3] * a.qscale;
+    }
+  }
+
+  // Keys this wave reads: its split's range, cut at the last position any
+  // row of the tile may see.
+  const int rlast = min(rt * 16 + 15, rows - 1);
+  const int kend = min(a.total, a.prefix + rlast / g + 1);
+  const int kbeg = split * a.split_keys;
+  const int kstop = min(kbeg + a.split_keys, kend);
+
+  float m = -__builtin_inff(), l = 0.f;
+  floatx4 acc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int last = a.total - 1;
+  for (int kt0 = kbeg; kt0 < kstop; kt0 += 16) {
+    // K row of key kt0 + j16 (its first DQ*grp floats skipped); V rows of keys
+    // kt0 + 4 grp + r.  Positions past the sequence are clamped to its last
+    // key: always a valid address, and masked below.
+    float kf[DQ];
+    floatx4 vf[4][DB / 4];
+    if constexpr (BLK16) {
+      // B % 16 == 0: the 16 keys of the tile share one block.
+      const int j = kt0 / a.block_size;
+      unsigned blk = (unsigned)a.table[j];
+      blk = blk < (unsigned)a.num_blocks ? blk : (unsigned)(a.num_blocks - 1);
+      const int64_t hb = (int64_t)blk * a.p_ld_blk + (int64_t)kvh * a.p_ld_head;
+      const int o0 = j * a.block_size;
+      const float* kr = a.kp + hb + (int64_t)(min(kt0 + j16, last) - o0) * a.p_ld_off + DQ * grp;
+#pragma unroll
+      for (int i = 0; i < DQ / 4; ++i) {
+        const floatx4 t = ld4(kr + 4 * i);
+        kf[4 * i + 0] = t[0]; kf[4 * i + 1] = t[1]; kf[4 * i + 2] = t[2]; kf[4 * i + 3] = t[3];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vr = a.vp + hb + (int64_t)(min(kt0 + 4 * grp + r, last) - o0) * a.p_ld_off + DB * j16;
+#pragma unroll
+        for (int i = 0; i < DB / 4; ++i) vf[r][i] = ld4(vr + 4 * i);
+      }
+    } else {
+      const float* kr = key_row(a.kp, a, kvh, min(kt0 + j16, last)) + DQ * grp;
+#pragma unroll
+      for (int i = 0; i < DQ / 4; ++i) {
+        const floatx4 t = ld4(kr + 4 * i);
+        kf[4 * i + 0] = t[0]; kf[4 * i + 1] = t[1]; kf[4 * i + 2] = t[2]; kf[4 * i + 3] = t[3];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vr = key_row(a.vp, a, kvh, min(kt0 + 4 * grp + r, last)) + DB * j16;
+#pragma unroll
+        for (int i = 0; i < DB / 4; ++i) vf[r][i] = ld4(vr + 4 * i);
+      }
+    }
+
+    floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qv[i], s, 0, 0, 0);
+
+    // Causal mask (covers positions past the sequence: qpos <= total - 1).
+    float sv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sv[r] = (kt0 + 4 * grp + r > qpos) ? -__builtin_inff() : s[r];
+    float mx = __builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3]));
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = __builtin_fmaxf(m, mx);
+    const float msafe = mnew == -__builtin_inff() ? 0.f : mnew;
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sv[r] - msafe);
+    const float corr = __builtin_amdgcn_exp2f(m - msafe);
+    float ps = (p[0] + p[1]) + (p[2] + p[3]);
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * corr + ps;
+    m = mnew;
+#pragma unroll
+    for (int i = 0; i < DB; ++i) acc[i] *= corr;
+
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r][i / 4][i % 4], p[r], acc[i], 0, 0, 0);
+  }
+
+  if (!rvalid) return;
+  // Lane holds O^T[4 grp + r'][row] of d-block i: d = DB (4 grp + r') + i.
+  if (a.splits == 1) {
+    const float inv = 1.f / l;
+    float* op = a.out + (int64_t)head * a.o_ld_head + (int64_t)c * a.o_ld_tok;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* dst = op + DB * (4 * grp + r);
+#pragma unroll
+      for (int i = 0; i < DB / 4; ++i) {
+        floatx4 t;
+        t[0] = acc[4 * i + 0][r] * inv; t[1] = acc[4 * i + 1][r] * inv;
+        t[2] = acc[4 * i + 2][r] * inv; t[3] = acc[4 * i + 3][r] * inv;
+        *reinterpret_cast<floatx4*>(dst + 4 * i) = t;
+      }
+    }
+  } else {
+    const int64_t rowg = (int64_t)split * a.rows_total + (int64_t)kvh * rows + rho;
+    float* wp = a.ws_acc + rowg * D;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* dst = wp + DB * (4 * grp + r);
+#pragma unroll
+      for (int i = 0; i < DB / 4; ++i) {
+        floatx4 t;
+        t[0] = acc[4 * i + 0][r]; t[1] = acc[4 * i + 1][r];
+        t[2] = acc[4 * i + 2][r]; t[3] = acc[4 * i + 3][r];
+        *reinterpret_cast<floatx4*>(dst + 4 * i) = t;
+      }
+    }
+    if (grp == 0) {
+      a.ws_ml[2 * rowg + 0] = m;
+      a.ws_ml[2 * rowg + 1] = l;
+    }
+  }
+}
+
+// Merges the splits of one row: M = max m_s, out = sum acc_s 2^(m_s - M) /
+// sum l_s 2^(m_s - M) (a split that saw no visible key has m = -inf, l = 0).
+template <int D>
+__global__ __launch_bounds__(256) void attention_combine_kernel(const AttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows_total) return;
+  const int rows = a.group * a.chunk;
+  const int kvh = row / rows, rho = row - kvh * rows;
+  const int c = rho / a.group;
+  const int head = kvh * a.group + (rho - c * a.group);
+  float mx = -__builtin_inff();
+  for (int s = lane; s < a.splits; s += 64)
+    mx = __builtin_fmaxf(mx, a.ws_ml[2 * ((int64_t)s * a.rows_total + row)]);
+  mx = wave_max(mx);
+  const float msafe = mx == -__builtin_inff() ? 0.f : mx;
+  constexpr int PL = D / 64;   // d per lane
+  float o[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) o[i] = 0.f;
+  float lsum = 0.f;
+  for (int s = 0; s < a.splits; ++s) {
+    const int64_t rs = (int64_t)s * a.rows_total + row;
+    const float w = __builtin_amdgcn_exp2f(a.ws_ml[2 * rs] - msafe);
+    lsum += a.ws_ml[2 * rs + 1] * w;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) o[i] += a.ws_acc[rs * D + PL * lane + i] * w;
+  }
+  const float inv = 1.f / lsum;
+  float* op = a.out + (int64_t)head * a.o_ld_head + (int64_t)c * a.o_ld_tok + PL * lane;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) op[i] = o[i] * inv;
+}
+
+__global__ __launch_bounds__(256) void paged_kv_write_kernel(
+    const float* __restrict__ k, const float* __restrict__ v, int tokens, int heads, int d4,
+    int64_t s_tok, int64_t s_head, const int64_t* __restrict__ slots, float* __restrict__ kp,
+    float* __restrict__ vp, int64_t nslots, int block_size, int64_t p_ld_blk, int64_t p_ld_head,
+    int64_t p_ld_off) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)tokens * heads * d4) return;
+  const int q4 = (int)(i % d4);
+  const int64_t th = i / d4;
+  const int h = (int)(th % heads);
+  const int t = (int)(th / heads);
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot >= nslots) return;
+  const int64_t blk = slot / block_size, off = slot - blk * block_size;
+  const int64_t src = (int64_t)t * s_tok + (int64_t)h * s_head + 4 * q4;
+  const int64_t dst = blk * p_ld_blk + (int64_t)h * p_ld_head + off * p_ld_off + 4 * q4;
+  *reinterpret_cast<floatx4*>(kp + dst) = *reinterpret_cast<const floatx4*>(k + src);
+  *reinterpret_cast<floatx4*>(vp + dst) = *reinterpret_cast<const floatx4*>(v + src);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int D>
+int launch_attention(const AttnArgs& a, bool blk16, hipStream_t st) {
+  const int blocks = (a.items + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock;
+  if (blk16)
+    chunked_attention_kernel<D, true><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);
+  else
+    chunked_attention_kernel<D, false><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);
+  if (a.splits > 1)
+    attention_combine_kernel<D><<<(a.rows_total + 3) / 4, 256, 0, st>>>(a);
+  return kq_check_launch("chunked_attention");
+}
+
+}  // namespace
+
+extern "C" size_t kq_chunked_attention_workspace_bytes(int64_t q_heads, int64_t kv_heads,
+                                                       int64_t chunk_len, int64_t head_dim,
+                                                       int64_t prefix_len) {
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || chunk_len <= 0 ||
+      head_dim <= 0 || prefix_len < 0)
+    return 0;
+  const AttnPlan p = attn_plan(q_heads, kv_heads, chunk_len, prefix_len);
+  if (p.splits <= 1) return 0;
+  return (size_t)p.splits * (size_t)(q_heads * chunk_len) * (size_t)(head_dim + 2) * sizeof(float);
+}
+
+extern "C" int kq_chunked_attention_f32(
+    const float* q, int64_t q_heads, int64_t chunk_len, int64_t head_dim, int64_t q_ld_head,
+    int64_t q_ld_tok, const float* k_pool, const float* v_pool, int64_t kv_heads,
+    int64_t num_blocks, int64_t block_size, int64_t pool_ld_blk, int64_t pool_ld_head,
+    int64_t pool_ld_off, const int32_t* block_table, int64_t table_len, int64_t prefix_len,
+    float* out, int64_t out_ld_head, int64_t out_ld_tok, void* workspace,
+    size_t workspace_bytes, kq_stream_t stream) {
+  KQ_REQUIRE(q_heads > 0 && kv_heads > 0, "head counts must be positive");
+  KQ_REQUIRE(q_heads % kv_heads == 0, "GQA requires q_heads % kv_heads == 0");
+  KQ_REQUIRE(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128");
+  KQ_REQUIRE(chunk_len >= 0 && prefix_len >= 0, "chunk_len and prefix_len must be >= 0");
+  KQ_REQUIRE(block_size > 0 && num_blocks > 0, "block_size and num_blocks must be positive");
+  if (chunk_len == 0) return KQ_OK;
+  const int64_t total = prefix_len + chunk_len;
+  KQ_REQUIRE(table_len >= (total + block_size - 1) / block_size,
+             "block_table shorter than ceil((prefix_len + chunk_len) / block_size)");
+  KQ_REQUIRE(total < (int64_t(1) << 30) && q_heads * chunk_len < (int64_t(1) << 30),
+             "sequence too long");
+  KQ_REQUIRE(q && k_pool && v_pool && block_table && out, "null pointer");
+  KQ_REQUIRE(aligned16(q) && aligned16(k_pool) && aligned16(v_pool) && aligned16(out),
+             "q, pools and out must be 16-byte aligned");
+  KQ_REQUIRE(q_ld_head % 4 == 0 && q_ld_tok % 4 == 0 && out_ld_head % 4 == 0 &&
+                 out_ld_tok % 4 == 0 && pool_ld_blk % 4 == 0 && pool_ld_head % 4 == 0 &&
+                 pool_ld_off % 4 == 0,
+             "strides must be multiples of 4 elements");
+  const AttnPlan p = attn_plan(q_heads, kv_heads, chunk_len, prefix_len);
+  AttnArgs a{};
+  a.q = q; a.kp = k_pool; a.vp = v_pool; a.table = block_table; a.out = out;
+  a.q_ld_head = q_ld_head; a.q_ld_tok = q_ld_tok;
+  a.o_ld_head = out_ld_head; a.o_ld_tok = out_ld_tok;
+  a.p_ld_blk = pool_ld_blk; a.p_ld_head = pool_ld_head; a.p_ld_off = pool_ld_off;
+  a.num_blocks = (int)std::min<int64_t>(num_blocks, INT32_MAX);
+  a.block_size = (int)block_size;
+  a.group = (int)(q_heads / kv_heads);
+  a.chunk = (int)chunk_len; a.prefix = (int)prefix_len; a.total = (int)total;
+  a.rowtiles = (int)p.rowtiles; a.splits = (int)p.splits; a.split_keys = (int)p.split_keys;
+  a.items = (int)p.items; a.rows_total = (int)(q_heads * chunk_len);
+  a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+  if (p.splits > 1) {
+    const size_t need =
+        kq_chunked_attention_workspace_bytes(q_heads, kv_heads, chunk_len, head_dim, prefix_len);
+    if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+      return kq_set_error(KQ_ERR_WORKSPACE,
+                          "workspace missing, misaligned or smaller than "
+                          "kq_chunked_attention_workspace_bytes()");
+    a.ws_acc = static_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + (size_t)p.splits * a.rows_total * head_dim;
+  }
+  const bool blk16 = block_size % 16 == 0;
+  hipStream_t st = kq_stream(stream);
+  return head_dim == 64 ? launch_attention<64>(a, blk16, st) : launch_attention<128>(a, blk16, st);
+}
+
+extern "C" int kq_paged_kv_write_f32(const float* k, const float* v, int64_t tokens,
+                                     int64_t kv_heads, int64_t head_dim, int64_t src_ld_tok,
+                                     int64_t src_ld_head, const int64_t* slot_mapping,
+                                     float* k_pool, float* v_pool, int64_t num_blocks,
+                                     int64_t block_size, int64_t pool_ld_blk,
+                                     int64_t pool_ld_head, int64_t pool_ld_off,
+                                     kq_stream_t stream) {
+  KQ_REQUIRE(tokens >= 0 && kv_heads > 0 && head_dim > 0, "bad shape");
+  KQ_REQUIRE(head_dim % 4 == 0, "head_dim must be a multiple of 4");
+  KQ_REQUIRE(num_blocks > 0 && block_size > 0, "num_blocks and block_size must be positive");
+  if (tokens == 0) return KQ_OK;
+  KQ_REQUIRE(k && v && slot_mapping && k_pool && v_pool, "null pointer");
+  KQ_REQUIRE(aligned16(k) && aligned16(v) && aligned16(k_pool) && aligned16(v_pool),
+             "k, v and pools must be 16-byte aligned");
+  KQ_REQUIRE(src_ld_tok % 4 == 0 && src_ld_head % 4 == 0 && pool_ld_blk % 4 == 0 &&
+                 pool_ld_head % 4 == 0 && pool_ld_off % 4 == 0,
+             "strides must be multiples of 4 elements");
+  const int64_t n = tokens * kv_heads * (head_dim / 4);
+  KQ_REQUIRE(n < (int64_t(1) << 40) && tokens < INT32_MAX && block_size < INT32_MAX, "too large");
+  const int64_t blocks = (n + 255) / 256;
+  paged_kv_write_kernel<<<(unsigned)blocks, 256, 0, kq_stream(stream)>>>(
+      k, v, (int)tokens, (int)kv_heads, (int)(head_dim / 4), src_ld_tok, src_ld_head,
+      slot_mapping, k_pool, v_pool, num_blocks * block_size, (int)block_size, pool_ld_blk,
+      pool_ld_head, pool_ld_off);
+  return kq_check_launch("paged_kv_write");
+}

@@ -19,6 +19,6 @@ int kq_check_launch(const char* what) {
   return KQ_OK;
 }
 
-extern "C" int kq_version(void) { return 102; }
+extern "C" int kq_version(void) { return 103; }
 
 extern "C" const char* kq_last_error(void) { return g_last_error.c_str(); }
