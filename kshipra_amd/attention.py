@@ -165,7 +165,7 @@ def paged_kv_write(pool: torch.Tensor, layer: int, k: torch.Tensor, v: torch.Ten
     if k.shape != v.shape or k.shape[0] != H_kv or k.shape[2] != D:
         raise ValueError(f"k, v must be [{H_kv}, L, {D}], got {tuple(k.shape)}, {tuple(v.shape)}")
     if k.stride() != v.stride():
-        raise ValueError("k and v must have the same strides")
+        k, v = k.contiguous(), v.contiguous()
     if not -layers <= layer < layers:
         raise IndexError(f"layer {layer} is out of bounds for {layers} layers")
     layer = layer + layers if layer < 0 else layer

@@ -23,9 +23,11 @@
 // (P^T, k index l / 16) of the second product, so P never moves between
 // lanes.  Both reductions run in a permuted order chosen so every lane reads
 // contiguous memory: in the first product lane group q = l / 16 covers d in
-// [q D/4, (q+1) D/4) (D/16 float4 loads of its key's row), in the second lane
-// l % 16 = j covers d = (D/16) j + db, db = 0 .. D/16-1 (D/64 float4 loads per
-// key).  Row statistics (running max m, sum l) live in the lanes of their row;
+// [q D/4, (q+1) D/4) (D/16 float4 loads along its key's row), in the second
+// lane l % 16 = j covers d = (D/16) j + db, db = 0 .. D/16-1 (D/64 float4
+// loads per key).  (Spreading each load instruction over contiguous runs of
+// several lanes instead measured slower.)  Row statistics (running max m,
+// sum l) live in the lanes of their row;
 // one row's 16 scores are spread over lane groups, so the row max and sum take
 // two cross-lane steps.  Scores are in log2 units (Q is pre-scaled by
 // log2(e) / sqrt(D)) and exponentials are exp2.
@@ -42,7 +44,7 @@ namespace {
 
 constexpr int kAttnWavesPerBlock = 4;
 constexpr int64_t kAttnTargetWaves = 2048;     // 8 waves per CU on 256 CUs
-constexpr int64_t kAttnMinTilesPerSplit = 4;   // >= 64 keys per split
+constexpr int64_t kAttnMinTilesPerSplit = 1;
 constexpr int64_t kAttnMaxSplits = 256;
 
 struct AttnArgs {
@@ -99,8 +101,9 @@ __device__ __forceinline__ const float* key_row(const float* pool, const AttnArg
          (int64_t)(pos - j * a.block_size) * a.p_ld_off;
 }
 
+// Occupancy 3 (<= 168 registers per lane): measured faster than 2.
 template <int D, bool BLK16>
-__global__ __launch_bounds__(64 * kAttnWavesPerBlock) void chunked_attention_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * kAttnWavesPerBlock, 3) void chunked_attention_kernel(const AttnArgs a) {
   constexpr int DQ = D / 4;    // d per lane group in S^T = K Q^T
   constexpr int DB = D / 16;   // d-blocks of O^T (floats per lane per key in V)
   const int lane = threadIdx.x & 63;
@@ -150,51 +153,56 @@ __global__ __launch_bounds__(64 * kAttnWavesPerBlock) void chunked_attention_ker
 #pragma unroll
   for (int i = 0; i < DB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int last = a.total - 1;
-  for (int kt0 = kbeg; kt0 < kstop; kt0 += 16) {
-    // K row of key kt0 + j16 (its first DQ*grp floats skipped); V rows of keys
-    // kt0 + 4 grp + r.  Positions past the sequence are clamped to its last
-    // key: always a valid address, and masked below.
-    float kf[DQ];
-    floatx4 vf[4][DB / 4];
+  // Tile loads: K row of key kt0 + j16 (from d = DQ grp), V rows of keys
+  // kt0 + 4 grp + r (from d = DB j16).  Positions are clamped to the wave's
+  // last key, kstop - 1: inside a tile, positions >= kstop occur only when
+  // kstop is the causal / sequence end, where they are masked.  (Prefetching
+  // tile t + 1 during tile t measured slower: it doubles the K / V registers
+  // and drops occupancy from 3 to 2.)
+  const int lastk = kstop - 1;
+  struct Tile {
+    float k[DQ];
+    floatx4 v[4][DB / 4];
+  };
+  auto load = [&](Tile& t, int kt0) {
     if constexpr (BLK16) {
-      // B % 16 == 0: the 16 keys of the tile share one block.
-      const int j = kt0 / a.block_size;
+      // B % 16 == 0: the (clamped) keys of the tile share one block.
+      const int j = min(kt0, lastk) / a.block_size;
       unsigned blk = (unsigned)a.table[j];
       blk = blk < (unsigned)a.num_blocks ? blk : (unsigned)(a.num_blocks - 1);
       const int64_t hb = (int64_t)blk * a.p_ld_blk + (int64_t)kvh * a.p_ld_head;
       const int o0 = j * a.block_size;
-      const float* kr = a.kp + hb + (int64_t)(min(kt0 + j16, last) - o0) * a.p_ld_off + DQ * grp;
+      const float* kr = a.kp + hb + (int64_t)(min(kt0 + j16, lastk) - o0) * a.p_ld_off + DQ * grp;
 #pragma unroll
       for (int i = 0; i < DQ / 4; ++i) {
-        const floatx4 t = ld4(kr + 4 * i);
-        kf[4 * i + 0] = t[0]; kf[4 * i + 1] = t[1]; kf[4 * i + 2] = t[2]; kf[4 * i + 3] = t[3];
+        const floatx4 x = ld4(kr + 4 * i);
+        t.k[4 * i + 0] = x[0]; t.k[4 * i + 1] = x[1]; t.k[4 * i + 2] = x[2]; t.k[4 * i + 3] = x[3];
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float* vr = a.vp + hb + (int64_t)(min(kt0 + 4 * grp + r, last) - o0) * a.p_ld_off + DB * j16;
+        const float* vr = a.vp + hb + (int64_t)(min(kt0 + 4 * grp + r, lastk) - o0) * a.p_ld_off + DB * j16;
 #pragma unroll
-        for (int i = 0; i < DB / 4; ++i) vf[r][i] = ld4(vr + 4 * i);
+        for (int i = 0; i < DB / 4; ++i) t.v[r][i] = ld4(vr + 4 * i);
       }
     } else {
-      const float* kr = key_row(a.kp, a, kvh, min(kt0 + j16, last)) + DQ * grp;
+      const float* kr = key_row(a.kp, a, kvh, min(kt0 + j16, lastk)) + DQ * grp;
 #pragma unroll
       for (int i = 0; i < DQ / 4; ++i) {
-        const floatx4 t = ld4(kr + 4 * i);
-        kf[4 * i + 0] = t[0]; kf[4 * i + 1] = t[1]; kf[4 * i + 2] = t[2]; kf[4 * i + 3] = t[3];
+        const floatx4 x = ld4(kr + 4 * i);
+        t.k[4 * i + 0] = x[0]; t.k[4 * i + 1] = x[1]; t.k[4 * i + 2] = x[2]; t.k[4 * i + 3] = x[3];
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float* vr = key_row(a.vp, a, kvh, min(kt0 + 4 * grp + r, last)) + DB * j16;
+        const float* vr = key_row(a.vp, a, kvh, min(kt0 + 4 * grp + r, lastk)) + DB * j16;
 #pragma unroll
-        for (int i = 0; i < DB / 4; ++i) vf[r][i] = ld4(vr + 4 * i);
+        for (int i = 0; i < DB / 4; ++i) t.v[r][i] = ld4(vr + 4 * i);
       }
     }
-
+  };
+  auto compute = [&](const Tile& t, int kt0) {
     floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < DQ; ++i) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qv[i], s, 0, 0, 0);
-
+    for (int i = 0; i < DQ; ++i) s = __builtin_amdgcn_mfma_f32_16x16x4f32(t.k[i], qv[i], s, 0, 0, 0);
     // Causal mask (covers positions past the sequence: qpos <= total - 1).
     float sv[4];
 #pragma unroll
@@ -215,12 +223,17 @@ __global__ __launch_bounds__(64 * kAttnWavesPerBlock) void chunked_attention_ker
     m = mnew;
 #pragma unroll
     for (int i = 0; i < DB; ++i) acc[i] *= corr;
-
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
       for (int i = 0; i < DB; ++i)
-        acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r][i / 4][i % 4], p[r], acc[i], 0, 0, 0);
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(t.v[r][i / 4][i % 4], p[r], acc[i], 0, 0, 0);
+  };
+
+  for (int kt0 = kbeg; kt0 < kstop; kt0 += 16) {
+    Tile t;
+    load(t, kt0);
+    compute(t, kt0);
   }
 
   if (!rvalid) return;
@@ -260,38 +273,56 @@ __global__ __launch_bounds__(64 * kAttnWavesPerBlock) void chunked_attention_ker
   }
 }
 
-// Merges the splits of one row: M = max m_s, out = sum acc_s 2^(m_s - M) /
-// sum l_s 2^(m_s - M) (a split that saw no visible key has m = -inf, l = 0).
-template <int D>
+// Merges the splits of a row: M = max m_s, out = sum acc_s 2^(m_s - M) /
+// sum l_s 2^(m_s - M); a split that saw no visible key has m = -inf, l = 0.
+// A workgroup owns COLS float4 columns of one row; thread t takes column
+// t % COLS of splits t / COLS, t / COLS + SG, ... and the SG partial sums
+// meet in LDS.
+template <int D, int COLS>
 __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows_total) return;
+  constexpr int NV = D / 4;
+  constexpr int SG = 256 / COLS;
+  static_assert(NV % COLS == 0, "columns");
+  __shared__ float red[4];
+  __shared__ floatx4 po[256];
+  __shared__ float pl[SG];
+  const int t = threadIdx.x;
+  const int row = blockIdx.x / (NV / COLS);
+  const int v4 = (blockIdx.x % (NV / COLS)) * COLS + t % COLS;
+  const int sg = t / COLS;
+  float mx = -__builtin_inff();
+  for (int s = t; s < a.splits; s += 256)
+    mx = __builtin_fmaxf(mx, a.ws_ml[2 * ((int64_t)s * a.rows_total + row)]);
+  mx = wave_max(mx);
+  if ((t & 63) == 0) red[t >> 6] = mx;
+  __syncthreads();
+  mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+  const float msafe = mx == -__builtin_inff() ? 0.f : mx;
+  floatx4 o = {0.f, 0.f, 0.f, 0.f};
+  float ls = 0.f;
+#pragma unroll 4
+  for (int s = sg; s < a.splits; s += SG) {
+    const int64_t rs = (int64_t)s * a.rows_total + row;
+    const float w = __builtin_amdgcn_exp2f(a.ws_ml[2 * rs] - msafe);
+    ls += a.ws_ml[2 * rs + 1] * w;
+    o += ld4(a.ws_acc + rs * D + 4 * v4) * w;
+  }
+  po[t] = o;
+  if (t % COLS == 0) pl[sg] = ls;
+  __syncthreads();
+  if (t >= COLS) return;
+  floatx4 sum = po[t];
+  float lsum = pl[0];
+  for (int g = 1; g < SG; ++g) {
+    sum += po[g * COLS + t];
+    lsum += pl[g];
+  }
   const int rows = a.group * a.chunk;
   const int kvh = row / rows, rho = row - kvh * rows;
   const int c = rho / a.group;
   const int head = kvh * a.group + (rho - c * a.group);
-  float mx = -__builtin_inff();
-  for (int s = lane; s < a.splits; s += 64)
-    mx = __builtin_fmaxf(mx, a.ws_ml[2 * ((int64_t)s * a.rows_total + row)]);
-  mx = wave_max(mx);
-  const float msafe = mx == -__builtin_inff() ? 0.f : mx;
-  constexpr int PL = D / 64;   // d per lane
-  float o[PL];
-#pragma unroll
-  for (int i = 0; i < PL; ++i) o[i] = 0.f;
-  float lsum = 0.f;
-  for (int s = 0; s < a.splits; ++s) {
-    const int64_t rs = (int64_t)s * a.rows_total + row;
-    const float w = __builtin_amdgcn_exp2f(a.ws_ml[2 * rs] - msafe);
-    lsum += a.ws_ml[2 * rs + 1] * w;
-#pragma unroll
-    for (int i = 0; i < PL; ++i) o[i] += a.ws_acc[rs * D + PL * lane + i] * w;
-  }
-  const float inv = 1.f / lsum;
-  float* op = a.out + (int64_t)head * a.o_ld_head + (int64_t)c * a.o_ld_tok + PL * lane;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) op[i] = o[i] * inv;
+  *reinterpret_cast<floatx4*>(a.out + (int64_t)head * a.o_ld_head + (int64_t)c * a.o_ld_tok +
+                              4 * v4) = sum * (1.f / lsum);
 }
 
 __global__ __launch_bounds__(256) void paged_kv_write_kernel(
@@ -323,8 +354,14 @@ int launch_attention(const AttnArgs& a, bool blk16, hipStream_t st) {
     chunked_attention_kernel<D, true><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);
   else
     chunked_attention_kernel<D, false><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);
-  if (a.splits > 1)
-    attention_combine_kernel<D><<<(a.rows_total + 3) / 4, 256, 0, st>>>(a);
+  if (a.splits > 1) {
+    // Few rows with many splits (decode): 4 columns per workgroup, 64 split
+    // groups; many rows with few splits: one workgroup per row.
+    if (a.splits >= 32)
+      attention_combine_kernel<D, 4><<<a.rows_total * (D / 16), 256, 0, st>>>(a);
+    else
+      attention_combine_kernel<D, D / 4><<<a.rows_total, 256, 0, st>>>(a);
+  }
   return kq_check_launch("chunked_attention");
 }
 

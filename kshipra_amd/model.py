@@ -11,9 +11,15 @@ decoder that runs every projection through ``QuantizedLinear`` on the GPU.
   of ``KshipraModel.forward`` (``engine/model.py:93-151``) and the greedy loop
   of ``generate`` (``:153-205``): one prefill forward over the prompt (M = prompt
   length), then M = 1 decode steps, first-index argmax.  The seven projections
-  of each layer are ``QuantizedLinear`` modules (the hot path); RMSNorm, RoPE,
-  attention over a contiguous KV cache and the fp32 lm_head are plain torch
-  ops on the same device and stream.  With ``fuse=True`` q/k/v run as one
+  of each layer are ``QuantizedLinear`` modules (the hot path).  K / V live in
+  the reference's block pool [num_blocks, layers, 2, H_kv, B, D] (B =
+  ``block_size``, 64 as in ``generate``; block table = identity, slot of
+  position p = table[p // B] * B + p % B, ``engine/model.py:163-197``) and
+  each layer stores its chunk with ``paged_kv_write`` and attends with the
+  HIP ``chunked_attention`` (``engine/model.py:124-140``);
+  ``attention="dense"`` keeps a contiguous cache and plain torch attention
+  instead (for comparisons).  RMSNorm, RoPE and the fp32 lm_head are plain
+  torch ops on the same device and stream.  With ``fuse=True`` q/k/v run as one
   ``FusedQuantizedLinear`` launch (same weights, row-stacked) and gate/up with
   the SiLU gate as one ``FusedGateUpSiLU`` launch (intermediate size a
   multiple of 16; else a ``FusedQuantizedLinear`` and torch's silu * up).
@@ -37,6 +43,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .attention import chunked_attention, paged_kv_write
 from .quantization import (FusedGateUpSiLU, FusedQuantizedLinear, QuantizedLinear, QuantizedWeight,
                            quantize_int4_per_group, quantize_int8_per_channel, quantized_linear,
                            quantized_linear_argmax)
@@ -100,13 +107,20 @@ class DecoderLM:
     def __init__(self, cfg: DecoderConfig, weights: Dict[str, torch.Tensor], scheme: str,
                  device: torch.device, group_size: int = 128, max_seq: int = 256,
                  fuse: bool = False, lm_head_scheme: Optional[str] = None,
-                 quantized: Optional[Dict[str, "QuantizedWeight"]] = None) -> None:
+                 quantized: Optional[Dict[str, "QuantizedWeight"]] = None,
+                 block_size: int = 64, attention: str = "paged") -> None:
         """``quantized``: name (``layers.{i}.{proj}``) -> QuantizedWeight already
         on ``device`` (e.g. from kshipra_amd.checkpoint.load_quantized_weights);
         those projections are used as they are and their float weights are not
         needed in ``weights``."""
+        if attention not in ("paged", "dense"):
+            raise ValueError(f"attention must be 'paged' or 'dense', got {attention!r}")
+        if block_size <= 0:
+            raise ValueError("block_size must be positive")
         self.cfg = cfg
         self.device = device
+        self.attention = attention
+        self.block_size = block_size
         dev = lambda t: torch.as_tensor(t).to(device=device, dtype=torch.float32)
         self.embed = dev(weights["embed_tokens.weight"])
         self.norm = dev(weights["norm.weight"])
@@ -167,10 +181,19 @@ class DecoderLM:
 
     def reset(self) -> None:
         c = self.cfg
-        shape = (c.num_layers, c.num_kv_heads, self.max_seq, c.head_dim)
-        self.k_cache = torch.zeros(shape, dtype=torch.float32, device=self.device)
-        self.v_cache = torch.zeros(shape, dtype=torch.float32, device=self.device)
         self.pos = 0
+        if self.attention == "dense":
+            shape = (c.num_layers, c.num_kv_heads, self.max_seq, c.head_dim)
+            self.k_cache = torch.zeros(shape, dtype=torch.float32, device=self.device)
+            self.v_cache = torch.zeros(shape, dtype=torch.float32, device=self.device)
+            return
+        # engine/model.py:165-177: pool sized for the whole sequence, identity table
+        B = self.block_size
+        nb = (self.max_seq + B - 1) // B
+        self.pool = torch.zeros((nb, c.num_layers, 2, c.num_kv_heads, B, c.head_dim),
+                                dtype=torch.float32, device=self.device)
+        self.block_table = list(range(nb))
+        self.table_dev = torch.tensor(self.block_table, dtype=torch.int32, device=self.device)
 
     @torch.inference_mode()
     def forward(self, ids: List[int]) -> torch.Tensor:
@@ -196,9 +219,16 @@ class DecoderLM:
         g = c.num_heads // c.num_kv_heads
         scale = 1.0 / math.sqrt(c.head_dim)
         S = self.pos + L
-        qpos = torch.arange(self.pos, S, device=self.device)
-        kpos = torch.arange(S, device=self.device)
-        mask = kpos[None, :] > qpos[:, None]
+        if self.attention == "dense":
+            qpos = torch.arange(self.pos, S, device=self.device)
+            kpos = torch.arange(S, device=self.device)
+            mask = kpos[None, :] > qpos[:, None]
+        else:
+            B = self.block_size
+            slots = torch.tensor([self.block_table[p // B] * B + p % B for p in range(self.pos, S)],
+                                 dtype=torch.int64, device=self.device)
+            attn_buf = torch.empty((L, c.num_heads, c.head_dim), dtype=torch.float32,
+                                   device=self.device)
         for li, layer in enumerate(self.layers):
             res = h
             x = _rms_norm(h, layer["in_norm"], c.rms_norm_eps)
@@ -211,14 +241,20 @@ class DecoderLM:
             v = v.reshape(L, c.num_kv_heads, c.head_dim).transpose(0, 1)
             q = q * cos[None] + _rotate_half(q) * sin[None]
             k = k * cos[None] + _rotate_half(k) * sin[None]
-            self.k_cache[li, :, self.pos:S] = k
-            self.v_cache[li, :, self.pos:S] = v
-            kc = self.k_cache[li, :, :S].repeat_interleave(g, dim=0).contiguous()
-            vc = self.v_cache[li, :, :S].repeat_interleave(g, dim=0).contiguous()
-            s = torch.matmul(q.contiguous(), kc.transpose(1, 2).contiguous()) * scale
-            s = s.masked_fill(mask[None], float("-inf"))
-            p = torch.softmax(s, dim=-1)
-            a = torch.matmul(p, vc).transpose(0, 1).reshape(L, c.num_heads * c.head_dim)
+            if self.attention == "dense":
+                self.k_cache[li, :, self.pos:S] = k
+                self.v_cache[li, :, self.pos:S] = v
+                kc = self.k_cache[li, :, :S].repeat_interleave(g, dim=0).contiguous()
+                vc = self.v_cache[li, :, :S].repeat_interleave(g, dim=0).contiguous()
+                s = torch.matmul(q.contiguous(), kc.transpose(1, 2).contiguous()) * scale
+                s = s.masked_fill(mask[None], float("-inf"))
+                p = torch.softmax(s, dim=-1)
+                a = torch.matmul(p, vc).transpose(0, 1).reshape(L, c.num_heads * c.head_dim)
+            else:
+                paged_kv_write(self.pool, li, k, v, slots)
+                chunked_attention(q, self.pool[:, li, 0], self.pool[:, li, 1], self.table_dev,
+                                  self.pos, L, self.block_size, out=attn_buf.transpose(0, 1))
+                a = attn_buf.view(L, c.num_heads * c.head_dim)
             h = res + layer["o_proj"](a.contiguous())
             res = h
             x = _rms_norm(h, layer["post_norm"], c.rms_norm_eps)

@@ -21,12 +21,14 @@ from oracle import decoder as odec
 pytestmark = pytest.mark.gpu
 
 
-def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed, fuse=False, lm_head_scheme=None):
+def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed, fuse=False, lm_head_scheme=None,
+                   **attn):
     w = decoder_weights(cfg_dict, seed=seed)
     ocfg = odec.DecoderConfig(**cfg_dict)
     gcfg = DecoderConfig(**cfg_dict)
     gpu_lm = DecoderLM(gcfg, {k: torch.from_numpy(v) for k, v in w.items()}, scheme, gpu,
-                       max_seq=len(prompt) + new_tokens + 1, fuse=fuse, lm_head_scheme=lm_head_scheme)
+                       max_seq=len(prompt) + new_tokens + 1, fuse=fuse, lm_head_scheme=lm_head_scheme,
+                       **attn)
     toks_g, logits_g = gpu_lm.generate(prompt, new_tokens)
     oracle_lm = odec.OracleDecoder(ocfg, w, scheme, lm_head_scheme=lm_head_scheme)
     toks_o, logits_o = oracle_lm.generate(prompt, new_tokens)
@@ -37,7 +39,7 @@ def _greedy_parity(gpu, cfg_dict, scheme, prompt, new_tokens, seed, fuse=False, 
         top2 = np.sort(lo)[-2:]
         min_gap = min(min_gap, float(top2[1] - top2[0]))
     print(f"[{scheme} L={cfg_dict['num_layers']} prompt={len(prompt)} fuse={fuse} "
-          f"lm_head={lm_head_scheme}] tokens {toks_g} "
+          f"lm_head={lm_head_scheme} {attn}] tokens {toks_g} "
           f"logit rel dev {worst:.3e} min top-2 gap {min_gap:.3e}", flush=True)
     assert toks_g == toks_o
     assert worst < 1e-3
@@ -71,6 +73,22 @@ def test_long_prompt_uses_gemm_prefill(gpu, scheme):
     cfg = dict(QWEN05B, num_layers=4, vocab_size=32000)
     prompt = [int(t) for t in np.random.default_rng(1).integers(0, 32000, 48)]
     _greedy_parity(gpu, cfg, scheme, prompt, 6, seed=1)
+
+
+@pytest.mark.parametrize("scheme", ["int4", "int8"])
+def test_paged_pool_small_blocks(gpu, scheme):
+    """K / V in a block pool of 16-token blocks: the 40-token prefill spans
+    three blocks (several 16-row attention tiles) and decode crosses the next
+    block boundary (engine/model.py:124-140 with the generate loop's slots)."""
+    cfg = dict(QWEN05B, num_layers=4, vocab_size=32000)
+    prompt = [int(t) for t in np.random.default_rng(2).integers(0, 32000, 40)]
+    _greedy_parity(gpu, cfg, scheme, prompt, 12, seed=2, fuse=True, block_size=16)
+
+
+def test_dense_attention_option(gpu):
+    """attention="dense" (contiguous cache, torch attention) gives the same tokens."""
+    cfg = dict(QWEN05B, num_layers=4, vocab_size=32000)
+    _greedy_parity(gpu, cfg, "int4", [1, 42, 100, 201, 7, 999], 6, seed=3, attention="dense")
 
 
 def test_hf_projection_swap(gpu):
