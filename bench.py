@@ -18,6 +18,8 @@ Also reported (same JSON line):
     [14336 x 4096], then [512 x 14336] through down);
   * lm_head [128256 x 4096] INT8 / INT4 at M = 1 and 32: the GEMV alone,
     followed by torch.argmax, and with the greedy argmax fused into it;
+  * paged K/V chunked attention with Llama-3-8B heads over a 32-layer block
+    pool: decode at 4096 / 16384 context (GB/s) and prefill chunks (TFLOP/s);
   * ``roofline``: the kernel that dominates the headline step (the fused
     gate/up dequant-GEMV, [28672 x 4096]) vs the 8 TB/s HBM peak, with its
     HBM traffic from the rocprofv3 counter summary under profiles/;
@@ -26,7 +28,7 @@ Also reported (same JSON line):
     host's cores over one layer (7 projections).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--eager] [--quick]
-                       [--only all|prefill|lm_head]
+                       [--only all|prefill|lm_head|attention]
 """
 
 from __future__ import annotations
@@ -290,6 +292,45 @@ def lm_head(dev, steps, warmup, eager):
     return out
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def attention(dev, steps, warmup, eager):
+    """Paged K/V attention with Llama-3-8B heads (32 query / 8 KV heads, D = 128)
+    over a 32-layer block pool [blocks, 32, 2, 8, 64, 128] fp32: one
+    chunked_attention call per layer (graph of 32), each layer's K / V distinct
+    in HBM.  Decode (1 query) reports K/V GB/s; prefill chunks report TFLOP/s
+    (4 * H_q * D * visible (query, key) pairs)."""
+    from kshipra_amd.attention import chunked_attention
+    hq, hkv, d, b, layers = 32, 8, 128, 64, 32
+    out = {}
+    for name, c, p in (("decode_ctx4096", 1, 4095), ("decode_ctx16384", 1, 16383),
+                       ("prefill_chunk512_after3584", 512, 3584), ("prefill_chunk2048", 2048, 0)):
+        nb = (p + c + b - 1) // b
+        pool = torch.randn((nb, layers, 2, hkv, b, d), device=dev)
+        q = torch.randn((layers, hq, c, d), device=dev)
+        o = torch.empty((layers, hq, c, d), device=dev)
+        table = torch.arange(nb, dtype=torch.int32, device=dev)
+
+        def run():
+            for li in range(layers):
+                chunked_attention(q[li], pool[:, li, 0], pool[:, li, 1], table, p, c, b, out=o[li])
+
+        ms = time_steps(graph_or_eager(run, eager), steps, warmup) / layers
+        kv_bytes = 2 * hkv * (p + c) * d * 4 + 2 * hq * c * d * 4
+        flops = 4 * hq * d * (c * p + c * (c + 1) // 2)
+        r = {"us_per_layer": round(ms * 1e3, 2), "gbs": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
+             "tflops": round(flops / (ms * 1e-3) / 1e12, 2)}
+        if c == 1:
+            r["frac_of_hbm_peak"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+        else:
+            r["frac_of_fp32_mfma_peak"] = round(r["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4)
+        out[name] = r
+        del pool, q, o
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(layer, budget_s=20.0):
     """The oracle's restatement of QuantizedLinear.forward (materialise the fp32
     weight, then fp32 BLAS), on this host's cores, over one layer at M = 1."""
@@ -337,7 +378,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
     ap.add_argument("--layers", type=int, default=LAYERS,
                     help="layers in the sweep (fewer only for counter runs; the headline uses 32)")
-    ap.add_argument("--only", choices=("all", "prefill", "lm_head"), default="all",
+    ap.add_argument("--only", choices=("all", "prefill", "lm_head", "attention"), default="all",
                     help="profiling aid: run one section and print its figures only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -354,6 +395,9 @@ def main():
             print(json.dumps({"section": "int4_prefill_m512_mlp", "tflops": round(pf["tflops"], 1),
                               "ms": round(pf["ms"], 4), "gflop": round(pf["gflop"], 1),
                               "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}))
+        elif args.only == "attention":
+            print(json.dumps({"section": "attention_llama3_8b_heads",
+                              "results": attention(dev, args.steps, args.warmup, args.eager)}))
         else:
             print(json.dumps({"section": "lm_head_128256x4096",
                               "results": lm_head(dev, args.steps, args.warmup, args.eager)}))
@@ -414,6 +458,7 @@ def main():
                                               "gflop": round(pf["gflop"], 1),
                                               "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}
         breakdown["lm_head_128256x4096"] = lm_head(dev, args.steps, args.warmup, args.eager)
+        breakdown["attention_llama3_8b_heads"] = attention(dev, max(args.steps // 2, 3), 1, args.eager)
         cpu = cpu_baseline(int4[0])
 
     # a plain 1 GiB device copy: the reference point for HBM-traffic counters

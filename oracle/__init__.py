@@ -15,6 +15,9 @@ Contents
 ``decoder``  a numpy fp32 decoder step (RMSNorm, q/k/v, RoPE, causal GQA
              attention, o, SiLU-gated MLP, final norm, lm_head, argmax) in the
              op order of ``engine/model.py:93-205``, used for greedy-token parity.
+``attention`` the paged K/V store (``engine/model.py:124-129``), the chunked
+             online-softmax attention (``engine/chunked_prefill.py:93-140``)
+             and the monolithic masked softmax (``:47-90``), float64.
 
 How the oracle is pinned (each check is in ``tests/test_oracle_*.py``):
 
@@ -28,5 +31,8 @@ How the oracle is pinned (each check is in ``tests/test_oracle_*.py``):
 * brute force over all 256 packed bytes for unpack / sign restore;
 * the fp32 -> fp16 conversion against numpy's independent implementation over
   every fp16 boundary and tie;
-* C restatement == numpy restatement on seeded random weights.
+* C restatement == numpy restatement on seeded random weights;
+* attention: chunked == monolithic on the reference tests' configurations
+  (its own golden relation) and closed forms (single key, equal keys, a
+  dominant key, the GQA head map, the causal mask).
 """

@@ -21,9 +21,13 @@ CPU = torch.device("cpu")
 def test_workspace_plan():
     lib = _lib.load()
     ws = lib.kq_chunked_attention_workspace_bytes
-    # Llama-3-8B decode at 4096 keys: 8 KV heads x one row tile -> 64 key
-    # splits of 64 keys, each keeping (acc[128], m, l) per query row
-    assert ws(32, 8, 1, 128, 4095) == 64 * 32 * 1 * 130 * 4
+    # Llama-3-8B decode at 4096 keys: 8 KV heads x one row tile -> 256 key
+    # splits of one 16-key tile, each keeping (acc[128], m, l) per query row
+    assert ws(32, 8, 1, 128, 4095) == 256 * 32 * 1 * 130 * 4
+    # 16384 keys: still 256 splits (the cap), of 4 tiles each
+    assert ws(32, 8, 1, 128, 16383) == 256 * 32 * 1 * 130 * 4
+    # 1024 keys: 64 one-tile splits
+    assert ws(32, 8, 1, 128, 1023) == 64 * 32 * 1 * 130 * 4
     # short context: a single split, no workspace
     assert ws(32, 8, 1, 128, 10) == 0
     # long prefill chunk: 8 x 1024 row tiles fill the GPU unsplit
