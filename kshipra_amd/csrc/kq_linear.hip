@@ -198,11 +198,27 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     const uint8_t* wq, const uint16_t* sc, int64_t row_bytes,
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
     const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
-    int2* __restrict__ argp, int pairs) {
+    int2* __restrict__ argp, int pairs, int64_t split_units, int64_t split_ystride) {
   static_assert(!M1 || (A_LDS && HL && !REM), "single-row instances stage in LDS, pre-loads only");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int TPU = BITS == 4 ? 4 : 2;  // k-steps per unit
   const int M = M1 ? 1 : M_;
+  // K split across blockIdx.y: workgroup row z owns units [z s, (z + 1) s)
+  // (s = split_units) -- its columns of x, payload (64 bytes per unit of a
+  // row, both schemes) and INT4 group scales -- and writes its partial sums
+  // (row scale applied, no bias) to y + z * split_ystride.
+  if constexpr (!M1) {
+    if (gridDim.y > 1) {
+      const int64_t u0 = (int64_t)blockIdx.y * split_units;
+      const int64_t c0 = u0 * (BITS == 4 ? 128 : 64);
+      x += c0;
+      K = K - c0 < split_units * (BITS == 4 ? 128 : 64) ? K - c0 : split_units * (BITS == 4 ? 128 : 64);
+      wq += u0 * 64;
+      if constexpr (BITS == 4) sc += u0;
+      nunits = nunits - u0 < split_units ? nunits - u0 : split_units;
+      y += (int64_t)blockIdx.y * split_ystride;
+    }
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwaves = blockDim.x >> 6;
@@ -325,7 +341,9 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     // Everything else: four entries per lane at a time, their loads issued
     // together so the latencies overlap.  Skipped (wave-uniformly) when the
     // pre-loads covered every entry, so no wait for the weights is emitted.
-    if (REM && (ntot > 64 * pre_n || !xvec || (K & 7) != 0)) {
+    // (K short of the units' columns: the pre-loads skipped the K-tail
+    // entries, which are staged here with zeros past K.)
+    if (REM && (ntot > 64 * pre_n || !xvec || K != nunits * (BITS == 4 ? 128 : 64))) {
       for (int j0 = 0; 64 * j0 < ntot; j0 += 4) {
         float raw8[4][8];
         bool need[4];
@@ -1121,6 +1139,8 @@ constexpr int64_t kSkinnyMinGroups = 192;
 constexpr int64_t kSkinnyOneRound = 4096;       // waves resident at once (4 per SIMD x 1024 SIMDs)
 constexpr int64_t kSkinnyLdsA = 160 * 1024;  // LDS per CU (gfx950), all usable by one workgroup
 constexpr int64_t kSkinnyLdsSmall = 64 * 1024;  // staging this small never limits residency
+constexpr int64_t kSkinnySplitMinM = 4;         // K split across workgroups from this M
+constexpr int64_t kSkinnySplitMinK = 8192;      // ... and this K
 constexpr int64_t kCUs = 256;
 constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
 constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
@@ -1154,12 +1174,16 @@ struct Plan {
   int64_t mpad = 0;     // gemm: operand-plane rows (M rounded up to the row tile)
   bool wspec = false;   // gemm: warp-specialized DMA kernel (prefill chunks)
   int64_t pitch = 0;    // skinny: entries per (quad, A-row) in the lane-major layout
+  int64_t ksplit = 1;   // skinny: K slices across workgroup rows (partials + reduction when > 1)
+  int64_t split_units = 0;  // skinny: units per K slice
   size_t ws = 0;        // workspace bytes
 };
 
 // pairs: N rows interleave gate and up weights by 16-row tiles; a skinny
 // plan then takes exactly two tiles per wave (one gate / up pair).
-Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp, bool pairs = false) {
+// split: the caller can take a K-split skinny plan (plain linear only).
+Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp, bool pairs = false,
+               bool split = false) {
   Plan p;
   const bool tiled = bits == 4 ? (g == 128) : (k % 64 == 0);
   if (!tiled) { p.path = Path::Generic; return p; }
@@ -1185,20 +1209,51 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
       p.nt = 2;
       p.pairs = true;
     }
-    const int64_t ntiles = (n + 16 * p.nt - 1) / (16 * p.nt);
-    auto waves_for = [&](int64_t pw) { return ntiles * ((p.nunits + pw - 1) / pw); };
+    const int64_t tpu = bits == 4 ? 4 : 2;
+    // K split (tall K, M >= 4): every workgroup stages all of x for its
+    // columns, i.e. M x K activations per 16 * NT columns.  When that cannot
+    // stay in LDS with the grid resident, or the shape allows fewer than 4
+    // tiles per workgroup, workgroups take 4 tiles and a K slice small enough
+    // that its staging stays <= 64 KiB, with enough slices for one workgroup
+    // per CU; partial sums are added in slice order by a reduction.  The
+    // reduction launch and the partials cost ~3 us, so (measured on the
+    // Llama-3-8B shapes) this pays only from K = 8192 and M = 4 (down_proj
+    // at M = 8: 34 -> 23 us INT8, 28 -> 23 us INT4); shorter K loses.
+    int64_t units = p.nunits;
+    if (split && m >= kSkinnySplitMinM && k >= kSkinnySplitMinK && !pairs) {
+      const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
+      const int64_t full = 128 * ((p.nT + 1) | 1) * m;
+      const bool fits = full <= kSkinnyLdsSmall ||
+                        (full <= kSkinnyLdsA && (kSkinnyLdsA / full) * kCUs >= groups);
+      if (!fits || p.nt < 4) {
+        const int64_t tiles4 = (n + 63) / 64;
+        auto slice = [&](int64_t s) { return (p.nunits + s - 1) / s; };
+        int64_t s = 1;
+        while (s < p.nunits &&
+               (tiles4 * s < kCUs || 128 * ((slice(s) * tpu + 1) | 1) * m > kSkinnyLdsSmall))
+          ++s;
+        if (s > 1) {
+          p.nt = 4;
+          units = slice(s);
+          p.ksplit = (p.nunits + units - 1) / units;
+        }
+      }
+    }
+    p.split_units = units;
+    const int64_t ntiles = (n + 16 * p.nt - 1) / (16 * p.nt) * p.ksplit;
+    auto waves_for = [&](int64_t pw) { return ntiles * ((units + pw - 1) / pw); };
     int64_t best_pw = 2;
     for (int64_t pw = 8; pw >= 2; pw /= 2) {
       if (waves_for(pw) >= kSkinnyMinWaves) { best_pw = pw; break; }
     }
-    if ((p.nunits + 7) / 8 > kSkinnyMaxWaves || waves_for(8) > kSkinnyMaxTotalWaves) best_pw = 16;
-    while ((p.nunits + best_pw - 1) / best_pw > kSkinnyMaxWaves && best_pw < 16) best_pw *= 2;
+    if ((units + 7) / 8 > kSkinnyMaxWaves || waves_for(8) > kSkinnyMaxTotalWaves) best_pw = 16;
+    while ((units + best_pw - 1) / best_pw > kSkinnyMaxWaves && best_pw < 16) best_pw *= 2;
     p.per_wave = best_pw;
     const int64_t maxw = std::min<int64_t>(best_pw, 16 / p.nt) * p.nt >= 16 ? kSkinnyMaxWaves16
                                                                            : kSkinnyMaxWaves;
-    p.waves = (int)std::min<int64_t>((p.nunits + best_pw - 1) / best_pw, maxw);
-    if ((int64_t)p.waves * best_pw < p.nunits)          // long K: several KS-unit batches
-      p.per_wave = (p.nunits + p.waves - 1) / p.waves;
+    p.waves = (int)std::min<int64_t>((units + best_pw - 1) / best_pw, maxw);
+    if ((int64_t)p.waves * best_pw < units)          // long K: several KS-unit batches
+      p.per_wave = (units + p.waves - 1) / p.waves;
     p.ks = (int)std::min<int64_t>(best_pw, 16 / p.nt);
     // M = 1: two tiles per wave in 4-unit batches and 8 waves per workgroup
     // halve the activation staging per column (it reads all of x per
@@ -1219,10 +1274,10 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
         p.ks = 4;
       }
     }
-    p.svec = bits == 4 && p.per_wave % p.ks == 0 && (kp / 128) % p.ks == 0;
+    p.svec = bits == 4 && p.per_wave % p.ks == 0 && (kp / 128) % p.ks == 0 && units % p.ks == 0;
     // An odd pitch puts the four lane quads of an LDS row in different banks;
     // column nT is a pad column (written with unused values, never read).
-    p.pitch = (p.nT + 1) | 1;
+    p.pitch = (units * tpu + 1) | 1;
     // Staged activations: 2 halves x 16 B x 4 quads per entry.  Above 64 KiB
     // they limit how many workgroups a CU holds; stage in LDS then only if
     // the whole grid is still resident at once (else a second round of
@@ -1235,6 +1290,7 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
     }
     if (!p.a_lds) p.pitch = p.nT;
     p.ws = p.a_lds ? 0 : (size_t)(128 * p.pitch * m);
+    if (p.ksplit > 1) p.ws = (size_t)(4 * p.ksplit * m * n);   // partials (staging is in LDS)
     return p;
   }
   const int64_t keff = p.nT * 32;
@@ -1285,7 +1341,7 @@ void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStrea
 #define KQ_SKINNY(KS_, NT_)                                                                   \
   skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC, M1, REM><<<grid, block, shm, st>>>(            \
       x, ldx, (int)m, k, xvec, wq, sc, row_bytes, ng, p.nunits, p.per_wave, (int)p.pitch, xa, \
-      bias, y, ldy, n, argp, pairs)
+      bias, y, ldy, n, argp, pairs, p.split_units, m * n)
   if (p.nt == 4) {
     if (p.ks == 2) KQ_SKINNY(2, 4); else KQ_SKINNY(4, 4);
   } else if (p.nt == 2) {
@@ -1325,7 +1381,17 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   const size_t red = (size_t)p.waves * p.nt * 256 * sizeof(float);
   const size_t abytes = p.a_lds ? (size_t)(128 * p.pitch * m) : 0;
   const size_t shm = std::max(red, abytes);
-  const dim3 grid((unsigned)((n + 16 * p.nt - 1) / (16 * p.nt)));
+  const dim3 grid((unsigned)((n + 16 * p.nt - 1) / (16 * p.nt)), (unsigned)p.ksplit);
+  // K split: the slices write partials (row scale applied, no bias) to the
+  // workspace, [slice][m][n]; the reduction adds them in slice order + bias.
+  float* const y_out = y;
+  const int64_t ldy_out = ldy;
+  const float* const bias_out = bias;
+  if (p.ksplit > 1) {
+    y = static_cast<float*>(ws);
+    ldy = n;
+    bias = nullptr;
+  }
   const dim3 block((unsigned)(64 * p.waves));
   const bool svec = p.svec && reinterpret_cast<uintptr_t>(sc) % (2 * p.ks) == 0;
 #define KQ_SKINNY_SV(LDS_, HL_, M1_, REM_)                                                      \
@@ -1344,8 +1410,12 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   // single-row instances are used for INT4 (measured: INT8 runs as fast or
   // faster through the general ones).
   constexpr int kTpu = BITS == 4 ? 4 : 2;
+  constexpr int64_t kUnitCols = BITS == 4 ? 128 : 64;
   const int pre1 = std::min(4, std::max(1, p.ks * kTpu / 16));
-  const bool aligned = xvec && k % 8 == 0;
+  // Instances without the remainder block need every entry pre-loadable:
+  // aligned x and no K tail inside the last unit (an INT4 K that is not a
+  // multiple of 128 leaves tail entries that must be staged as zeros).
+  const bool aligned = xvec && k == p.nunits * kUnitCols;
   const bool one_row = BITS == 4 && aligned && m == 1 && p.per_wave * kTpu <= 16 * pre1;
   const bool covered = aligned && m * p.per_wave * kTpu <= 16 * 4;
   if (p.a_lds) {
@@ -1363,6 +1433,15 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
     else KQ_SKINNY_SV(false, false, false, false);
   }
 #undef KQ_SKINNY_SV
+  if (p.ksplit > 1) {
+    const bool vec = n % 4 == 0 && ldy_out % 4 == 0 && reinterpret_cast<uintptr_t>(y_out) % 16 == 0 &&
+                     (bias_out == nullptr || reinterpret_cast<uintptr_t>(bias_out) % 16 == 0);
+    const int64_t items = vec ? m * n / 4 : m * n;
+    const unsigned rg = (unsigned)std::min<int64_t>((items + 255) / 256, 8192);
+    // BITS = 4 instance: sums only (the slices applied any INT8 row scale)
+    if (vec) splitk_reduce_kernel<4, true><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, nullptr, bias_out, y_out, ldy_out);
+    else splitk_reduce_kernel<4, false><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, nullptr, bias_out, y_out, ldy_out);
+  }
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }
 
@@ -1458,10 +1537,10 @@ int check_linear_args(const float* x, int64_t m, int64_t ldx, const void* wq, co
 extern "C" size_t kq_linear_workspace_bytes(int scheme, int64_t m, int64_t n, int64_t k,
                                             int64_t group_size) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
-  if (scheme == 8) return make_plan(8, m, n, k, 0, k).ws;
+  if (scheme == 8) return make_plan(8, m, n, k, 0, k, false, true).ws;
   if (group_size <= 0) return 0;
   const int64_t kp = (k + group_size - 1) / group_size * group_size;
-  return make_plan(4, m, n, k, group_size, kp).ws;
+  return make_plan(4, m, n, k, group_size, kp, false, true).ws;
 }
 
 extern "C" int kq_linear_int8(const float* x, int64_t m, int64_t ldx, const int8_t* payload,
@@ -1469,7 +1548,7 @@ extern "C" int kq_linear_int8(const float* x, int64_t m, int64_t ldx, const int8
                               int64_t n, int64_t k, void* ws, size_t ws_bytes,
                               kq_stream_t stream) {
   if (int s = check_linear_args(x, m, ldx, payload, scales, y, ldy, n, k)) return s;
-  const Plan p = make_plan(8, m, n, k, 0, k);
+  const Plan p = make_plan(8, m, n, k, 0, k, false, true);
   if (p.ws > 0 && (ws == nullptr || ws_bytes < p.ws))
     return kq_set_error(KQ_ERR_WORKSPACE, "workspace missing or smaller than kq_linear_workspace_bytes()");
   const uint8_t* wq = reinterpret_cast<const uint8_t*>(payload);
@@ -1488,7 +1567,7 @@ extern "C" int kq_linear_int4(const float* x, int64_t m, int64_t ldx, const uint
   if (int s = check_linear_args(x, m, ldx, payload, scales, y, ldy, n, k)) return s;
   KQ_REQUIRE(g > 0 && g % 2 == 0, "group_size must be a positive even integer");
   KQ_REQUIRE(kp % g == 0 && kp >= k && kp - k < g, "inconsistent in_features_padded");
-  const Plan p = make_plan(4, m, n, k, g, kp);
+  const Plan p = make_plan(4, m, n, k, g, kp, false, true);
   if (p.ws > 0 && (ws == nullptr || ws_bytes < p.ws))
     return kq_set_error(KQ_ERR_WORKSPACE, "workspace missing or smaller than kq_linear_workspace_bytes()");
   const int64_t ng = kp / g;

@@ -83,6 +83,35 @@ def _run(gpu, m, n, k, scheme, g=128, bias=True, seed=0, outliers=False):
 def test_skinny_paths(gpu, scheme, m):
     _run(gpu, m, 272, 896, scheme, seed=m)              # K = 896: 7 groups / 14 windows
     _run(gpu, m, 100, 4864, scheme, seed=m + 50)        # N % 16 != 0, odd unit counts
+    # INT4: K = 4000 ends 32 columns into its last group (the tail is staged as
+    # zeros; regression for stale staging there); INT8 takes the generic path
+    _run(gpu, m, 200, 4000, scheme, seed=m + 90)
+
+
+@pytest.mark.parametrize("m,n,k,scheme", [
+    (4, 4096, 14336, "int4"),    # down_proj: 4 K slices of 28 groups
+    (8, 4096, 14336, "int8"),    # 8 slices of 28 windows
+    (16, 4096, 14336, "int4"),   # split rows (no hi / lo pairing), 16 slices
+    (12, 1000, 8100, "int4"),    # K tail inside the last slice, N % 64 != 0
+    (5, 300, 9024, "int8"),      # 47 slices of 3 windows
+    (2, 4096, 14336, "int4"),    # below the split's M: whole-K workgroups
+    (8, 28672, 4096, "int4"),    # below the split's K: whole-K workgroups
+])
+def test_skinny_k_split(gpu, m, n, k, scheme):
+    """Skinny launches whose K is split across workgroup rows (partials in the
+    workspace, reduced in slice order with the bias), and their unsplit
+    neighbours: aligned activations with bias, unaligned without."""
+    w = gaussian((n, k), seed=n + k + m)
+    b = gaussian((n,), seed=n + k + m + 1)
+    wt = torch.from_numpy(w).to(gpu)
+    qw = quantize_int8_per_channel(wt) if scheme == "int8" else quantize_int4_per_group(wt, 128)
+    del wt
+    xs = torch.from_numpy(gaussian((m, k + 1), seed=n + k + m + 2, std=1.0)).to(gpu)
+    for name, x, bias in (("aligned", xs[:, :k].contiguous(), b), ("unaligned", xs[:, 1:], None)):
+        y = quantized_linear(x, qw, None if bias is None else torch.from_numpy(bias).to(gpu))
+        torch.cuda.synchronize()
+        y64, mag = _reference(x.cpu().numpy(), w, scheme, 128, bias)
+        _compare(y, y64, mag, f"k-split {scheme} m={m} n={n} k={k} {name}")
 
 
 @pytest.mark.parametrize("n,k,scheme", [
