@@ -4,7 +4,7 @@ Reference value: ``x @ (q * s)^T + b`` in float64 over the oracle's exact
 dequantized weight (engine/quantization.py:394-396 evaluated without
 rounding).  Bars, written per test:
 
-* norm-wise:     max|y - y64| / max|y64|            <= 1e-4   (north star: 1e-3)
+* norm-wise:     max|y - y64| / max|y64|            <= 1e-4   (the target is 1e-3)
 * element-wise:  |y - y64| <= 1e-4 * (|x| @ |w_hat|^T + |b|)  (condition-aware,
                  so outputs that cancel to ~0 are still checked)
 
