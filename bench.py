@@ -362,11 +362,24 @@ def cpu_baseline(layer, budget_s=20.0):
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
     cores = blas_threads or os.cpu_count()
+    # The same with one BLAS thread (the reference harness pins one thread).
+    t1 = None
+    if threadpool_limits is not None:
+        with threadpool_limits(limits=1, user_api="blas"):
+            one_pass()
+            t1s = []
+            for _ in range(2):
+                t0 = time.perf_counter()
+                one_pass()
+                t1s.append(time.perf_counter() - t0)
+        t1 = float(np.median(t1s))
     return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": int(cores), "kind": "port",
             "sample": (f"one Llama-3-8B layer (7 projections, INT4 G=128, M=1): numpy "
                        f"dequantize (1 thread) + OpenBLAS fp32 GEMV ({cores} threads); median of "
                        f"{len(times)} passes, {t * 1e3:.1f} ms/layer; host {os.cpu_count()} CPUs"),
-            "ms_per_layer": t * 1e3}
+            "ms_per_layer": t * 1e3,
+            "value_1_thread": None if t1 is None else nbytes / t1 / 1e9,
+            "ms_per_layer_1_thread": None if t1 is None else t1 * 1e3}
 
 
 def main():
