@@ -44,6 +44,7 @@ namespace {
 
 constexpr int kAttnWavesPerBlock = 4;
 constexpr int64_t kAttnTargetWaves = 2048;     // 8 waves per CU on 256 CUs
+constexpr int64_t kAttnSplitBelow = 512;       // split keys only below this many row-tile waves
 constexpr int64_t kAttnMinTilesPerSplit = 1;
 constexpr int64_t kAttnMaxSplits = 256;
 
@@ -74,8 +75,11 @@ AttnPlan attn_plan(int64_t hq, int64_t hkv, int64_t chunk, int64_t prefix) {
   p.rowtiles = (g * chunk + 15) / 16;
   const int64_t ntiles = (prefix + chunk + 15) / 16;
   const int64_t base = hkv * p.rowtiles;
+  // Row tiles alone fill the GPU from kAttnSplitBelow waves on (measured:
+  // the shared-tile kernel at 1024 waves beats 2 splits of the per-wave one
+  // by 18 %); decode and short chunks split their keys up to ~2048 waves.
   int64_t splits = 1;
-  if (base < kAttnTargetWaves) {
+  if (base < kAttnSplitBelow) {
     splits = (kAttnTargetWaves + base - 1) / base;
     splits = std::min(splits, (ntiles + kAttnMinTilesPerSplit - 1) / kAttnMinTilesPerSplit);
     splits = std::min(std::max<int64_t>(splits, 1), kAttnMaxSplits);
@@ -99,6 +103,44 @@ __device__ __forceinline__ const float* key_row(const float* pool, const AttnArg
   blk = blk < (unsigned)a.num_blocks ? blk : (unsigned)(a.num_blocks - 1);
   return pool + (int64_t)blk * a.p_ld_blk + (int64_t)kvh * a.p_ld_head +
          (int64_t)(pos - j * a.block_size) * a.p_ld_off;
+}
+
+// One 16-key tile of the online softmax for the 16 rows of a wave (lane
+// (j16, grp) = row j16; kf / vf: its K / V operands, qv: its pre-scaled Q):
+// S^T = K Q^T, causal mask key > qpos, running max / sum update, O^T += V^T P^T.
+template <int D>
+__device__ __forceinline__ void attn_tile(const float (&kf)[D / 4], const floatx4 (&vf)[4][D / 64],
+                                          const float (&qv)[D / 4], int kt0, int qpos, int grp,
+                                          float& m, float& l, floatx4 (&acc)[D / 16]) {
+  constexpr int DQ = D / 4, DB = D / 16;
+  floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < DQ; ++i) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qv[i], s, 0, 0, 0);
+  // Causal mask (covers positions past the sequence: qpos <= total - 1).
+  float sv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sv[r] = (kt0 + 4 * grp + r > qpos) ? -__builtin_inff() : s[r];
+  float mx = __builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3]));
+  mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float mnew = __builtin_fmaxf(m, mx);
+  const float msafe = mnew == -__builtin_inff() ? 0.f : mnew;
+  float p[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sv[r] - msafe);
+  const float corr = __builtin_amdgcn_exp2f(m - msafe);
+  float ps = (p[0] + p[1]) + (p[2] + p[3]);
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  l = l * corr + ps;
+  m = mnew;
+#pragma unroll
+  for (int i = 0; i < DB; ++i) acc[i] *= corr;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r][i / 4][i % 4], p[r], acc[i], 0, 0, 0);
 }
 
 // Occupancy 3 (<= 168 registers per lane): measured faster than 2.
@@ -199,41 +241,10 @@ __global__ __launch_bounds__(64 * kAttnWavesPerBlock, 3) void chunked_attention_
       }
     }
   };
-  auto compute = [&](const Tile& t, int kt0) {
-    floatx4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < DQ; ++i) s = __builtin_amdgcn_mfma_f32_16x16x4f32(t.k[i], qv[i], s, 0, 0, 0);
-    // Causal mask (covers positions past the sequence: qpos <= total - 1).
-    float sv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sv[r] = (kt0 + 4 * grp + r > qpos) ? -__builtin_inff() : s[r];
-    float mx = __builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3]));
-    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = __builtin_fmaxf(m, mx);
-    const float msafe = mnew == -__builtin_inff() ? 0.f : mnew;
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sv[r] - msafe);
-    const float corr = __builtin_amdgcn_exp2f(m - msafe);
-    float ps = (p[0] + p[1]) + (p[2] + p[3]);
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
-    l = l * corr + ps;
-    m = mnew;
-#pragma unroll
-    for (int i = 0; i < DB; ++i) acc[i] *= corr;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int i = 0; i < DB; ++i)
-        acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(t.v[r][i / 4][i % 4], p[r], acc[i], 0, 0, 0);
-  };
-
   for (int kt0 = kbeg; kt0 < kstop; kt0 += 16) {
     Tile t;
     load(t, kt0);
-    compute(t, kt0);
+    attn_tile<D>(t.k, t.v, qv, kt0, qpos, grp, m, l, acc);
   }
 
   if (!rvalid) return;
@@ -269,6 +280,148 @@ __global__ __launch_bounds__(64 * kAttnWavesPerBlock, 3) void chunked_attention_
     if (grp == 0) {
       a.ws_ml[2 * rowg + 0] = m;
       a.ws_ml[2 * rowg + 1] = l;
+    }
+  }
+}
+
+// Unsplit walks (prefill chunks): the 4 waves of a workgroup own 4
+// consecutive row tiles of one KV head and walk the same keys, so each
+// 16-key K / V tile is loaded once per workgroup -- all 256 threads, 4 KB
+// of it each (16 threads per key row) -- into a double-buffered LDS tile and
+// read from there by every wave (4x less L2 -> CU traffic than each wave
+// streaming its own copy).  The workgroup walks up to the last causal
+// position of its last row tile; a wave skips the math of tiles past its
+// own.  Rows are padded by D + 4 floats so the 16 rows one LDS read
+// instruction touches fall in different banks.
+template <int D>
+struct KvTileLds {
+  float k[16][D + 4];
+  float v[16][D + 4];
+};
+
+template <int D, bool BLK16>
+__global__ __launch_bounds__(64 * kAttnWavesPerBlock, 3) void chunked_attention_shared_kernel(const AttnArgs a) {
+  constexpr int DQ = D / 4, DB = D / 16;
+  constexpr int PF = D / 64;   // float4 of a K (and of a V) row per loading thread
+  static_assert(kAttnWavesPerBlock == 4, "256 loading threads: 16 per key row");
+  __shared__ KvTileLds<D> sm[2];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+
+  int b = blockIdx.x;
+  if ((gridDim.x & 7) == 0) b = (b & 7) * (gridDim.x >> 3) + (b >> 3);
+  const int rtb = (a.rowtiles + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock;
+  const int kvh = b / rtb;
+  const int rt0 = (b - kvh * rtb) * kAttnWavesPerBlock;
+  const int rt = rt0 + w;
+
+  const int g = a.group;
+  const int rows = g * a.chunk;
+  const int j16 = lane & 15, grp = lane >> 4;
+  const int rho = rt * 16 + j16;
+  const bool rvalid = rho < rows;
+  const int c = rvalid ? rho / g : 0;
+  const int head = kvh * g + (rvalid ? rho - c * g : 0);
+  const int qpos = a.prefix + c;
+
+  float qv[DQ];
+  {
+    const float* qp = a.q + (int64_t)head * a.q_ld_head + (int64_t)c * a.q_ld_tok + DQ * grp;
+#pragma unroll
+    for (int i = 0; i < DQ / 4; ++i) {
+      floatx4 t = rvalid ? ld4(qp + 4 * i) : floatx4{0.f, 0.f, 0.f, 0.f};
+      qv[4 * i + 0] = t[0] * a.qscale;
+      qv[4 * i + 1] = t[1] * a.qscale;
+      qv[4 * i + 2] = t[2] * a.qscale;
+      qv[4 * i + 3] = t[3] * a.qscale;
+    }
+  }
+
+  // Keys this wave's rows may see, and those of the workgroup's last row.
+  const int kend_w = rt * 16 < rows ? min(a.total, a.prefix + min(rt * 16 + 15, rows - 1) / g + 1) : 0;
+  const int rt_last = min(rt0 + kAttnWavesPerBlock - 1, a.rowtiles - 1);
+  const int kend = min(a.total, a.prefix + min(rt_last * 16 + 15, rows - 1) / g + 1);
+  const int lastk = kend - 1;
+
+  // Loader: thread t moves float4s [t % 16 * PF, +PF) of key row t / 16 of
+  // the tile (K and V); positions past the workgroup's keys are clamped to
+  // its last key (in bounds; masked or never used).
+  const int ck = threadIdx.x >> 4, cp = threadIdx.x & 15;
+  floatx4 kr[PF], vr[PF];
+  auto gload = [&](int kt0) {
+    const int pos = min(kt0 + ck, lastk);
+    const float* krow;
+    const float* vrow;
+    if constexpr (BLK16) {
+      const int j = min(kt0, lastk) / a.block_size;
+      unsigned blk = (unsigned)a.table[j];
+      blk = blk < (unsigned)a.num_blocks ? blk : (unsigned)(a.num_blocks - 1);
+      const int64_t off = (int64_t)blk * a.p_ld_blk + (int64_t)kvh * a.p_ld_head +
+                          (int64_t)(pos - j * a.block_size) * a.p_ld_off;
+      krow = a.kp + off;
+      vrow = a.vp + off;
+    } else {
+      krow = key_row(a.kp, a, kvh, pos);
+      vrow = key_row(a.vp, a, kvh, pos);
+    }
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      kr[i] = ld4(krow + 4 * (cp * PF + i));
+      vr[i] = ld4(vrow + 4 * (cp * PF + i));
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      *reinterpret_cast<floatx4*>(&sm[buf].k[ck][4 * (cp * PF + i)]) = kr[i];
+      *reinterpret_cast<floatx4*>(&sm[buf].v[ck][4 * (cp * PF + i)]) = vr[i];
+    }
+  };
+
+  float m = -__builtin_inff(), l = 0.f;
+  floatx4 acc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  int buf = 0;
+  for (int kt0 = 0; kt0 < kend; kt0 += 16) {
+    const bool more = kt0 + 16 < kend;
+    if (more) gload(kt0 + 16);          // next tile in flight during this one's math
+    if (kt0 < kend_w) {
+      float kf[DQ];
+      floatx4 vf[4][DB / 4];
+#pragma unroll
+      for (int i = 0; i < DQ / 4; ++i) {
+        const floatx4 x = *reinterpret_cast<const floatx4*>(&sm[buf].k[j16][DQ * grp + 4 * i]);
+        kf[4 * i + 0] = x[0]; kf[4 * i + 1] = x[1]; kf[4 * i + 2] = x[2]; kf[4 * i + 3] = x[3];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < DB / 4; ++i)
+          vf[r][i] = *reinterpret_cast<const floatx4*>(&sm[buf].v[4 * grp + r][DB * j16 + 4 * i]);
+      attn_tile<D>(kf, vf, qv, kt0, qpos, grp, m, l, acc);
+    }
+    if (more) sstore(buf ^ 1);          // the other buffer: last read before the previous barrier
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  if (!rvalid) return;
+  // Lane holds O^T[4 grp + r'][row] of d-block i: d = DB (4 grp + r') + i.
+  const float inv = 1.f / l;
+  float* op = a.out + (int64_t)head * a.o_ld_head + (int64_t)c * a.o_ld_tok;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float* dst = op + DB * (4 * grp + r);
+#pragma unroll
+    for (int i = 0; i < DB / 4; ++i) {
+      floatx4 t;
+      t[0] = acc[4 * i + 0][r] * inv; t[1] = acc[4 * i + 1][r] * inv;
+      t[2] = acc[4 * i + 2][r] * inv; t[3] = acc[4 * i + 3][r] * inv;
+      *reinterpret_cast<floatx4*>(dst + 4 * i) = t;
     }
   }
 }
@@ -349,6 +502,16 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 template <int D>
 int launch_attention(const AttnArgs& a, bool blk16, hipStream_t st) {
+  if (a.splits == 1) {
+    // Unsplit: workgroups of 4 row tiles sharing K / V tiles through LDS.
+    const int64_t rtb = (a.rowtiles + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock;
+    const int blocks = (int)(rtb * (a.rows_total / (a.group * a.chunk)));
+    if (blk16)
+      chunked_attention_shared_kernel<D, true><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);
+    else
+      chunked_attention_shared_kernel<D, false><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);
+    return kq_check_launch("chunked_attention");
+  }
   const int blocks = (a.items + kAttnWavesPerBlock - 1) / kAttnWavesPerBlock;
   if (blk16)
     chunked_attention_kernel<D, true><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);

@@ -30,8 +30,11 @@ def test_workspace_plan():
     assert ws(32, 8, 1, 128, 1023) == 64 * 32 * 1 * 130 * 4
     # short context: a single split, no workspace
     assert ws(32, 8, 1, 128, 10) == 0
-    # long prefill chunk: 8 x 1024 row tiles fill the GPU unsplit
+    # prefill chunks: >= 512 row-tile waves run unsplit (8 x 128 at 512 tokens)
     assert ws(32, 8, 4096, 128, 0) == 0
+    assert ws(32, 8, 512, 128, 3584) == 0
+    # a 64-token chunk (8 x 16 row tiles) still splits its keys
+    assert ws(32, 8, 64, 128, 1000) > 0
     # invalid shapes report 0 (the entry point rejects them)
     assert ws(6, 4, 1, 128, 100) == 0
     assert ws(32, 8, 0, 128, 100) == 0

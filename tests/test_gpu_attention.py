@@ -65,6 +65,10 @@ CASES = [
     (14, 2, 9, 70, 64, 12, True),        # g = 7, B not a multiple of 16
     (8, 8, 33, 40, 128, 5, True),        # g = 1, B = 5
     (2, 1, 3, 0, 64, 16, False),         # 3 queries, no prefix (pure causal)
+    # unsplit chunks: workgroups of 4 row tiles sharing K / V tiles in LDS
+    (28, 4, 300, 40, 128, 48, True),     # g = 7, B not a multiple of 16
+    (16, 16, 520, 20, 64, 20, True),     # g = 1, 33 row tiles (a partial workgroup)
+    (32, 8, 600, 1000, 128, 64, True),   # chunk after a long prefix, B = 64
 ]
 
 
