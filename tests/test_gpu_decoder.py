@@ -85,6 +85,15 @@ def test_paged_pool_small_blocks(gpu, scheme):
     _greedy_parity(gpu, cfg, scheme, prompt, 12, seed=2, fuse=True, block_size=16)
 
 
+def test_long_prompt_shared_tile_attention(gpu):
+    """A 600-token prompt: the prefill's attention runs as workgroups of 4 row
+    tiles sharing K / V tiles (7 x 600 rows per KV head), the decode steps
+    after it split their ~600 keys; INT4 projections through the GEMM path."""
+    cfg = dict(QWEN05B, num_layers=3, vocab_size=32000)
+    prompt = [int(t) for t in np.random.default_rng(4).integers(0, 32000, 600)]
+    _greedy_parity(gpu, cfg, "int4", prompt, 4, seed=4, fuse=True)
+
+
 def test_dense_attention_option(gpu):
     """attention="dense" (contiguous cache, torch attention) gives the same tokens."""
     cfg = dict(QWEN05B, num_layers=4, vocab_size=32000)
