@@ -612,7 +612,8 @@ extern "C" int kq_paged_kv_write_f32(const float* k, const float* v, int64_t tok
                  pool_ld_head % 4 == 0 && pool_ld_off % 4 == 0,
              "strides must be multiples of 4 elements");
   const int64_t n = tokens * kv_heads * (head_dim / 4);
-  KQ_REQUIRE(n < (int64_t(1) << 40) && tokens < INT32_MAX && block_size < INT32_MAX, "too large");
+  // one thread per 4 floats, 256 per workgroup: the grid must stay below 2^31 workgroups
+  KQ_REQUIRE(n < (int64_t(1) << 38) && tokens < INT32_MAX && block_size < INT32_MAX, "too large");
   const int64_t blocks = (n + 255) / 256;
   paged_kv_write_kernel<<<(unsigned)blocks, 256, 0, kq_stream(stream)>>>(
       k, v, (int)tokens, (int)kv_heads, (int)(head_dim / 4), src_ld_tok, src_ld_head,
