@@ -1135,10 +1135,12 @@ constexpr int kSkinnyMaxWaves16 = 8;          // with 16-unit batches (skinny_ma
 constexpr int64_t kSkinnyMinWaves = 2048;      // 8 waves per CU across 256 CUs
 constexpr int64_t kSkinnyMaxTotalWaves = 12288; // 48 per CU
 constexpr int kSkinnyNTMinM = 2;                // several 16-column tiles per workgroup from this M
+constexpr int kSkinnyNT4MinM = 5;               // ... four of them only from this M
 constexpr int64_t kSkinnyMinGroups = 192;
 constexpr int64_t kSkinnyOneRound = 4096;       // waves resident at once (4 per SIMD x 1024 SIMDs)
 constexpr int64_t kSkinnyLdsA = 160 * 1024;  // LDS per CU (gfx950), all usable by one workgroup
 constexpr int64_t kSkinnyLdsSmall = 64 * 1024;  // staging this small never limits residency
+constexpr int64_t kSkinnyLdsTwo = 80 * 1024;    // two workgroups per CU: LDS even over rounds
 constexpr int64_t kSkinnySplitMinM = 4;         // K split across workgroups from this M
 constexpr int64_t kSkinnySplitMinK = 8192;      // ... and this K
 constexpr int64_t kCUs = 256;
@@ -1249,6 +1251,16 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
     if ((units + 7) / 8 > kSkinnyMaxWaves || waves_for(8) > kSkinnyMaxTotalWaves) best_pw = 16;
     while ((units + best_pw - 1) / best_pw > kSkinnyMaxWaves && best_pw < 16) best_pw *= 2;
     p.per_wave = best_pw;
+    // Below M = 5, two tiles per workgroup instead of four, in 4-unit
+    // batches: the staging four tiles share is small there and twice the
+    // workgroups balance better (measured at M = 2 / 4, INT4: gate+up
+    // [28672 x 4096] 21.4 -> 17.3 / 22.5 -> 20.6 us, gate [14336 x 4096]
+    // 12.3 -> 10.6 us at M = 2).
+    if (p.nt == 4 && m >= 2 && m < kSkinnyNT4MinM && !pairs && p.ksplit == 1) {
+      p.nt = 2;
+      best_pw = std::max<int64_t>(best_pw, 4);
+      p.per_wave = best_pw;
+    }
     const int64_t maxw = std::min<int64_t>(best_pw, 16 / p.nt) * p.nt >= 16 ? kSkinnyMaxWaves16
                                                                            : kSkinnyMaxWaves;
     p.waves = (int)std::min<int64_t>((units + best_pw - 1) / best_pw, maxw);
@@ -1280,12 +1292,13 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
     p.pitch = (units * tpu + 1) | 1;
     // Staged activations: 2 halves x 16 B x 4 quads per entry.  Above 64 KiB
     // they limit how many workgroups a CU holds; stage in LDS then only if
-    // the whole grid is still resident at once (else a second round of
-    // workgroups waits: measured slower than staging by a pre-pass).
+    // two still fit a CU (<= 80 KiB: M = 4 at K = 4096) or the whole grid is
+    // resident at once (else, with one workgroup per CU and a second round
+    // waiting, measured slower than staging by a pre-pass).
     {
       const int64_t abytes = 128 * p.pitch * m;
       const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
-      p.a_lds = abytes <= kSkinnyLdsSmall ||
+      p.a_lds = abytes <= kSkinnyLdsSmall || abytes <= kSkinnyLdsTwo ||
                 (abytes <= kSkinnyLdsA && (kSkinnyLdsA / abytes) * kCUs >= groups);
     }
     if (!p.a_lds) p.pitch = p.nT;

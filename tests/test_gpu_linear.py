@@ -96,6 +96,8 @@ def test_skinny_paths(gpu, scheme, m):
     (5, 300, 9024, "int8"),      # 47 slices of 3 windows
     (2, 4096, 14336, "int4"),    # below the split's M: whole-K workgroups
     (8, 28672, 4096, "int4"),    # below the split's K: whole-K workgroups
+    (2, 28672, 4096, "int8"),    # M <= 4: two tiles per workgroup, LDS staging
+    (4, 14336, 4096, "int4"),    # 66 KiB staged per workgroup, two per CU
 ])
 def test_skinny_k_split(gpu, m, n, k, scheme):
     """Skinny launches whose K is split across workgroup rows (partials in the
