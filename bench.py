@@ -13,7 +13,7 @@ Also reported (same JSON line):
   * the same step with 7 separate launches per layer (224 per step);
   * INT8 per-channel M = 1 sweeps (same shapes);
   * per-projection GB/s (events around graphs of 32 same-shape launches);
-  * skinny / tiled M = 8 / 32 / 64 sweeps (continuous-batching decode);
+  * skinny / tiled M = 4 / 8 / 32 / 64 sweeps (continuous-batching decode);
   * INT4 prefill-chunk GEMM TFLOP/s (X [512 x 4096] through gate/up
     [14336 x 4096], then [512 x 14336] through down);
   * lm_head [128256 x 4096] INT8 / INT4 at M = 1 and 32: the GEMV alone,
@@ -457,7 +457,7 @@ def main():
             r = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[name])
             per8[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2)}
         breakdown["int8_m1_per_projection"] = per8
-        for m in (8, 32, 64):
+        for m in (4, 8, 32, 64):
             r = measure(int8, m, dev, max(args.steps // 2, 3), 1, args.eager)
             breakdown[f"int8_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
                                        "us_per_step": round(r["ms"] * 1e3, 1)}
