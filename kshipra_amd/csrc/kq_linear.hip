@@ -1141,7 +1141,7 @@ constexpr int64_t kSkinnyOneRound = 4096;       // waves resident at once (4 per
 constexpr int64_t kSkinnyLdsA = 160 * 1024;  // LDS per CU (gfx950), all usable by one workgroup
 constexpr int64_t kSkinnyLdsSmall = 64 * 1024;  // staging this small never limits residency
 constexpr int64_t kSkinnyLdsTwo = 80 * 1024;    // two workgroups per CU: LDS even over rounds
-constexpr int64_t kSkinnySplitMinM = 4;         // K split across workgroups from this M
+constexpr int64_t kSkinnySplitMinM = 3;         // K split across workgroups from this M
 constexpr int64_t kSkinnySplitMinK = 8192;      // ... and this K
 constexpr int64_t kCUs = 256;
 constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
@@ -1212,15 +1212,16 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
       p.pairs = true;
     }
     const int64_t tpu = bits == 4 ? 4 : 2;
-    // K split (tall K, M >= 4): every workgroup stages all of x for its
+    // K split (tall K, M >= 3): every workgroup stages all of x for its
     // columns, i.e. M x K activations per 16 * NT columns.  When that cannot
     // stay in LDS with the grid resident, or the shape allows fewer than 4
     // tiles per workgroup, workgroups take 4 tiles and a K slice small enough
     // that its staging stays <= 64 KiB, with enough slices for one workgroup
     // per CU; partial sums are added in slice order by a reduction.  The
     // reduction launch and the partials cost ~3 us, so (measured on the
-    // Llama-3-8B shapes) this pays only from K = 8192 and M = 4 (down_proj
-    // at M = 8: 34 -> 23 us INT8, 28 -> 23 us INT4); shorter K loses.
+    // Llama-3-8B shapes) this pays only from K = 8192 and M = 3 (down_proj
+    // at M = 3: 23.7 -> 19.7 us INT8; at M = 8: 34 -> 23 us INT8, 28 -> 23 us
+    // INT4); shorter K, and M = 2, lose.
     int64_t units = p.nunits;
     if (split && m >= kSkinnySplitMinM && k >= kSkinnySplitMinK && !pairs) {
       const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);

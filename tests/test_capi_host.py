@@ -52,11 +52,12 @@ def test_workspace_query_is_host_only():
     # workspace, 4 bytes per activation
     assert lib.kq_linear_workspace_bytes(8, 8, 4096, 4096, 0) == 0
     assert lib.kq_linear_workspace_bytes(8, 8, 28672, 4096, 0) == 4 * 8 * 4096
-    # K = 14336, M >= 4: K split into slices staged in LDS; the workspace
-    # holds one fp32 partial output per slice (8 slices at M = 8, 4 at M = 4)
+    # K = 14336, M >= 3: K split into slices staged in LDS; the workspace
+    # holds one fp32 partial output per slice (8 slices at M = 8, 4 at M = 4 and 3)
     assert lib.kq_linear_workspace_bytes(4, 8, 4096, 14336, 128) == 8 * 4 * 8 * 4096
     assert lib.kq_linear_workspace_bytes(8, 4, 4096, 14336, 0) == 4 * 4 * 4 * 4096
-    # ... below M = 4, whole-K workgroups stage x in LDS: no workspace
+    assert lib.kq_linear_workspace_bytes(8, 3, 4096, 14336, 0) == 4 * 4 * 3 * 4096
+    # ... below M = 3, whole-K workgroups stage x in LDS: no workspace
     assert lib.kq_linear_workspace_bytes(4, 2, 4096, 14336, 128) == 0
     # GEMM path: M rounded up to the 64-row tile
     assert lib.kq_linear_workspace_bytes(4, 512, 14336, 4096, 128) == 4 * 512 * 4096
