@@ -429,47 +429,67 @@ __global__ __launch_bounds__(64 * kAttnWavesPerBlock, 3) void chunked_attention_
 // Merges the splits of a row: M = max m_s, out = sum acc_s 2^(m_s - M) /
 // sum l_s 2^(m_s - M); a split that saw no visible key has m = -inf, l = 0.
 // A workgroup owns COLS float4 columns of one row; thread t takes column
-// t % COLS of splits t / COLS, t / COLS + SG, ... and the SG partial sums
-// meet in LDS.
+// t % COLS of splits t / COLS + j SG (j < kCombinePerThread), all loaded in
+// one round trip.  The row maximum is reduced across the workgroup, then
+// the SG partial sums of a column meet by shuffles within each wave (a
+// fixed xor tree) and across the 4 waves in LDS.
+constexpr int kCombinePerThread = 4;
 template <int D, int COLS>
 __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnArgs a) {
   constexpr int NV = D / 4;
   constexpr int SG = 256 / COLS;
-  static_assert(NV % COLS == 0, "columns");
+  static_assert(NV % COLS == 0 && 64 % COLS == 0, "columns");
   __shared__ float red[4];
-  __shared__ floatx4 po[256];
-  __shared__ float pl[SG];
-  const int t = threadIdx.x;
+  __shared__ floatx4 po[4][COLS];
+  __shared__ float pl[4][COLS];
+  const int t = threadIdx.x, wv = t >> 6;
   const int row = blockIdx.x / (NV / COLS);
   const int v4 = (blockIdx.x % (NV / COLS)) * COLS + t % COLS;
   const int sg = t / COLS;
-  float mx = -__builtin_inff();
-  for (int s = t; s < a.splits; s += 256)
-    mx = __builtin_fmaxf(mx, a.ws_ml[2 * ((int64_t)s * a.rows_total + row)]);
+  float ms[kCombinePerThread], lv[kCombinePerThread];
+  floatx4 av[kCombinePerThread];
+#pragma unroll
+  for (int j = 0; j < kCombinePerThread; j++) {
+    const int s = sg + j * SG;
+    const bool ok = s < a.splits;
+    // past the last split: read split 0 (in bounds) and discard it
+    const int64_t rs = (int64_t)(ok ? s : 0) * a.rows_total + row;
+    const float m = a.ws_ml[2 * rs], l = a.ws_ml[2 * rs + 1];
+    const floatx4 v = ld4(a.ws_acc + rs * D + 4 * v4);
+    ms[j] = ok ? m : -__builtin_inff();
+    lv[j] = ok ? l : 0.f;
+    av[j] = ok ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  float mx = ms[0];
+#pragma unroll
+  for (int j = 1; j < kCombinePerThread; j++) mx = __builtin_fmaxf(mx, ms[j]);
   mx = wave_max(mx);
-  if ((t & 63) == 0) red[t >> 6] = mx;
+  if ((t & 63) == 0) red[wv] = mx;
   __syncthreads();
   mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
   const float msafe = mx == -__builtin_inff() ? 0.f : mx;
   floatx4 o = {0.f, 0.f, 0.f, 0.f};
   float ls = 0.f;
-#pragma unroll 4
-  for (int s = sg; s < a.splits; s += SG) {
-    const int64_t rs = (int64_t)s * a.rows_total + row;
-    const float w = __builtin_amdgcn_exp2f(a.ws_ml[2 * rs] - msafe);
-    ls += a.ws_ml[2 * rs + 1] * w;
-    o += ld4(a.ws_acc + rs * D + 4 * v4) * w;
+#pragma unroll
+  for (int j = 0; j < kCombinePerThread; j++) {
+    const float w = __builtin_amdgcn_exp2f(ms[j] - msafe);
+    ls += lv[j] * w;
+    o += av[j] * w;
   }
-  po[t] = o;
-  if (t % COLS == 0) pl[sg] = ls;
+#pragma unroll
+  for (int off = COLS; off < 64; off <<= 1) {
+    ls += __shfl_xor(ls, off);
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] += __shfl_xor(o[i], off);
+  }
+  if ((t & 63) < COLS) {
+    po[wv][t & 63] = o;
+    pl[wv][t & 63] = ls;
+  }
   __syncthreads();
   if (t >= COLS) return;
-  floatx4 sum = po[t];
-  float lsum = pl[0];
-  for (int g = 1; g < SG; ++g) {
-    sum += po[g * COLS + t];
-    lsum += pl[g];
-  }
+  const floatx4 sum = (po[0][t] + po[1][t]) + (po[2][t] + po[3][t]);
+  const float lsum = (pl[0][t] + pl[1][t]) + (pl[2][t] + pl[3][t]);
   const int rows = a.group * a.chunk;
   const int kvh = row / rows, rho = row - kvh * rows;
   const int c = rho / a.group;
@@ -519,7 +539,10 @@ int launch_attention(const AttnArgs& a, bool blk16, hipStream_t st) {
     chunked_attention_kernel<D, false><<<blocks, 64 * kAttnWavesPerBlock, 0, st>>>(a);
   if (a.splits > 1) {
     // Few rows with many splits (decode): 4 columns per workgroup, 64 split
-    // groups; many rows with few splits: one workgroup per row.
+    // groups; many rows with few splits: one workgroup per row.  Either way
+    // each thread merges at most kCombinePerThread splits.
+    static_assert(kAttnMaxSplits <= kCombinePerThread * 64, "combine coverage (4 columns)");
+    static_assert(32 <= kCombinePerThread * (256 / (D / 4)), "combine coverage (one row)");
     if (a.splits >= 32)
       attention_combine_kernel<D, 4><<<a.rows_total * (D / 16), 256, 0, st>>>(a);
     else
