@@ -1064,13 +1064,28 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     float v[V];
 #pragma unroll
     for (int u = 0; u < V; u++) v[u] = 0.0f;
-    for (int zz = 0; zz < S; zz++) {
-      if constexpr (VEC) {
-        const float4 p = *reinterpret_cast<const float4*>(part + zz * total + o);
-        v[0] += p.x; v[1] += p.y; v[2] += p.z; v[3] += p.w;
-      } else {
-        v[0] += part[zz * total + o];
-      }
+    // Slices are added in order; the loads of up to 8 slices are issued
+    // before their adds, so 8 slices cost one memory round trip.
+    auto add = [&](const float4& p) { v[0] += p.x; if constexpr (VEC) { v[1] += p.y; v[2] += p.z; v[3] += p.w; } };
+    auto load = [&](int zz) {
+      if constexpr (VEC) return *reinterpret_cast<const float4*>(part + zz * total + o);
+      else return float4{part[zz * total + o], 0.0f, 0.0f, 0.0f};
+    };
+    int zz = 0;
+    for (; zz + 8 <= S; zz += 8) {
+      float4 p[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) p[j] = load(zz + j);
+#pragma unroll
+      for (int j = 0; j < 8; j++) add(p[j]);
+    }
+    if (zz < S) {
+      float4 p[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) p[j] = load(zz + j < S ? zz + j : zz);
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        if (zz + j < S) add(p[j]);
     }
 #pragma unroll
     for (int u = 0; u < V; u++) {
