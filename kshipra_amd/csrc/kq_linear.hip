@@ -14,8 +14,8 @@
 //    (deterministic).  The activations are staged as fp16 hi/lo MFMA operands
 //    in LDS by the workgroup itself when they fit, else by stage_skinny_kernel into
 //    the caller's workspace.
-//  * gemm_kernel    (M > 16, prefill chunks / batched decode): workgroup tile
-//    BM x 256; x is converted once per call into fp16 hi/lo operand planes
+//  * gemm_kernel    (17 <= M <= 32, batched decode): workgroup tile BM x 128
+//    (x 256 for very wide N); x is converted once per call into fp16 hi/lo operand planes
 //    (stage_planes_kernel), each 128-column stage of them is copied into LDS
 //    (double-buffered) and shared by the waves; each wave streams its own
 //    weight columns from HBM into registers one stage ahead.  K is split across workgroups when the tiles alone cannot
@@ -1159,8 +1159,13 @@ constexpr int64_t kSkinnyLdsTwo = 80 * 1024;    // two workgroups per CU: LDS ev
 constexpr int64_t kSkinnySplitMinM = 3;         // K split across workgroups from this M
 constexpr int64_t kSkinnySplitMinK = 8192;      // ... and this K
 constexpr int64_t kCUs = 256;
-constexpr int kGemmNTW = 4, kGemmWN = 4;     // workgroup tile BN = 256 columns
-constexpr int64_t kGemmBN = 16 * kGemmNTW * kGemmWN;
+constexpr int kGemmWN = 4;                    // waves per workgroup (one column strip each)
+// 16-column tiles per wave: two (BN = 128) unless that gives more than
+// kGemmNarrowMaxTiles column tiles, then four (BN = 256).  Measured at M =
+// 17-32 on the Llama-3-8B shapes: BN = 128 takes 2-4 us off down / o /
+// q+k+v (twice the workgroups, half the K splits and partials), BN = 256
+// is faster for lm_head (1002 narrow tiles).
+constexpr int64_t kGemmNarrowMaxTiles = 512;
 constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU
 constexpr int64_t kGemmMinStages = 4;       // stages per K split, at least
 constexpr int64_t kGemmWsMinM = 33;         // warp-specialized DMA kernel from this M
@@ -1180,6 +1185,7 @@ struct Plan {
   int64_t nunits = 0;   // INT4 groups / INT8 windows per row
   int64_t nT = 0;       // k-steps
   int mtw = 0;          // gemm: 16-row m-tiles per wave (BM = 16 * mtw)
+  int ntw = 4;          // gemm: 16-column tiles per wave (BN = 16 * ntw * kGemmWN)
   int64_t tiles_m = 0;  // gemm: workgroup tiles along M
   int64_t tiles_n = 0;  // gemm: workgroup tiles along N
   int64_t nstages = 0;  // gemm: 128-column K stages
@@ -1332,7 +1338,8 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
     const int64_t wide = (n + 64 * kWsWideNC - 1) / (64 * kWsWideNC);
     p.wsnc = bits == 4 && p.tiles_m * wide >= kWsWideMinTiles ? kWsWideNC : kWsNC;
   }
-  const int64_t bn = p.wspec ? 64 * p.wsnc : kGemmBN;
+  if (!p.wspec) p.ntw = (n + 16 * 2 * kGemmWN - 1) / (16 * 2 * kGemmWN) <= kGemmNarrowMaxTiles ? 2 : 4;
+  const int64_t bn = p.wspec ? 64 * p.wsnc : 16 * p.ntw * kGemmWN;
   p.tiles_n = (n + bn - 1) / bn;
   p.nstages = keff / 128;
   // Split K only as far as needed to give every CU two workgroups.
@@ -1474,12 +1481,12 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }
 
-template <int BITS, int MTW>
+template <int BITS, int MTW, int NTW>
 void launch_gemm_t(const Plan& p, const half8_t* planes, int64_t m, const uint8_t* wq,
                    const uint16_t* sc, int64_t row_bytes, int64_t ng, const float* bias, float* y,
                    int64_t ldy, int64_t n, float* part, hipStream_t st) {
   const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
-  gemm_kernel<BITS, MTW, kGemmNTW, kGemmWN><<<blocks, 64 * kGemmWN, 0, st>>>(
+  gemm_kernel<BITS, MTW, NTW, kGemmWN><<<blocks, 64 * kGemmWN, 0, st>>>(
       planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m, (int)p.tiles_n,
       p.gm, bias, y, ldy, n, part);
 }
@@ -1508,9 +1515,10 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
     }
 #undef KQ_WS
   } else if (p.mtw == 2) {
-    launch_gemm_t<BITS, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    if (p.ntw == 2) launch_gemm_t<BITS, 2, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    else launch_gemm_t<BITS, 2, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   } else {
-    launch_gemm_t<BITS, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    launch_gemm_t<BITS, 4, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   }
   if (part) {
     const bool vec = n % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
