@@ -1168,7 +1168,11 @@ constexpr int kGemmWN = 4;                    // waves per workgroup (one column
 constexpr int64_t kGemmNarrowMaxTiles = 512;
 constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU
 constexpr int64_t kGemmMinStages = 4;       // stages per K split, at least
-constexpr int64_t kGemmWsMinM = 33;         // warp-specialized DMA kernel from this M
+constexpr int64_t kGemmWsMinM = 33;         // warp-specialized DMA kernel from this M (INT4)
+// INT8 keeps gemm_kernel (64-row tiles above M = 32) up to M = 64: measured
+// at M = 33-64 on the Llama-3-8B shapes it is 2-13 us faster there (down,
+// gate/up, o, q+k+v, lm_head); for INT4 it loses on down and gate/up.
+constexpr int64_t kGemmWsMinM8 = 65;        // the same for INT8
 constexpr int64_t kGemmWsTargetBlocks = 256;  // one resident workgroup per CU (LDS ring)
 
 enum class Path { Skinny, Gemm, Generic };
@@ -1331,7 +1335,7 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
   const int64_t keff = p.nT * 32;
   if (keff % 128 != 0) { p.path = Path::Generic; return p; }
   p.path = Path::Gemm;
-  p.wspec = m >= kGemmWsMinM;
+  p.wspec = m >= (bits == 8 ? kGemmWsMinM8 : kGemmWsMinM);
   p.mtw = (m <= 32 && !p.wspec) ? 2 : 4;
   p.tiles_m = (m + 16 * p.mtw - 1) / (16 * p.mtw);
   if (p.wspec) {
@@ -1518,7 +1522,8 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
     if (p.ntw == 2) launch_gemm_t<BITS, 2, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
     else launch_gemm_t<BITS, 2, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   } else {
-    launch_gemm_t<BITS, 4, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    if (p.ntw == 2) launch_gemm_t<BITS, 4, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    else launch_gemm_t<BITS, 4, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   }
   if (part) {
     const bool vec = n % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
