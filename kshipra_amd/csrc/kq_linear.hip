@@ -1166,7 +1166,9 @@ constexpr int kGemmWN = 4;                    // waves per workgroup (one column
 // q+k+v (twice the workgroups, half the K splits and partials), BN = 256
 // is faster for lm_head (1002 narrow tiles).
 constexpr int64_t kGemmNarrowMaxTiles = 512;
-constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU
+constexpr int64_t kGemmTargetBlocks = 512;  // two resident workgroups per CU (INT4)
+constexpr int64_t kGemmTargetBlocks8 = 256; // INT8: one per CU (fewer K splits; measured
+                                            // 1-3 us faster at M = 17-64, INT4 loses)
 constexpr int64_t kGemmMinStages = 4;       // stages per K split, at least
 constexpr int64_t kGemmWsMinM = 33;         // warp-specialized DMA kernel from this M (INT4)
 // INT8 keeps gemm_kernel (64-row tiles above M = 32) up to M = 64: measured
@@ -1348,7 +1350,7 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
   p.nstages = keff / 128;
   // Split K only as far as needed to give every CU two workgroups.
   const int64_t tiles = p.tiles_m * p.tiles_n;
-  const int64_t target = p.wspec ? kGemmWsTargetBlocks : kGemmTargetBlocks;
+  const int64_t target = p.wspec ? kGemmWsTargetBlocks : (bits == 8 ? kGemmTargetBlocks8 : kGemmTargetBlocks);
   int64_t s = 1;
   if (tiles < target)
     s = std::max<int64_t>(1, std::min(target / tiles, p.nstages / kGemmMinStages));
