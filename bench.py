@@ -391,7 +391,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
     ap.add_argument("--layers", type=int, default=LAYERS,
                     help="layers in the sweep (fewer only for counter runs; the headline uses 32)")
-    ap.add_argument("--only", choices=("all", "prefill", "lm_head", "attention"), default="all",
+    ap.add_argument("--only", choices=("all", "prefill", "lm_head", "attention", "batch"), default="all",
                     help="profiling aid: run one section and print its figures only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -411,6 +411,18 @@ def main():
         elif args.only == "attention":
             print(json.dumps({"section": "attention_llama3_8b_heads",
                               "results": attention(dev, args.steps, args.warmup, args.eager)}))
+        elif args.only == "batch":
+            # decode batches: the 7-projection step at M = 8, 32, 64
+            res = {}
+            for scheme, seed in (("int8", 2), ("int4", 1)):
+                layers = build_layers(scheme, dev, seed=seed, nlayers=args.layers)
+                for m in (8, 32, 64):
+                    r = measure(layers, m, dev, args.steps, args.warmup, args.eager)
+                    res[f"{scheme}_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
+                                             "us_per_step": round(r["ms"] * 1e3, 1)}
+                del layers
+                torch.cuda.empty_cache()
+            print(json.dumps({"section": "decode_batches_llama3_8b", "results": res}))
         else:
             print(json.dumps({"section": "lm_head_128256x4096",
                               "results": lm_head(dev, args.steps, args.warmup, args.eager)}))
