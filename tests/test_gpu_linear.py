@@ -142,13 +142,13 @@ def test_m1_two_tile_waves(gpu, n, k, scheme):
 
 
 @pytest.mark.parametrize("scheme", ["int8", "int4"])
-@pytest.mark.parametrize("m", [17, 32, 64, 100, 256, 512])
+@pytest.mark.parametrize("m", [17, 32, 40, 64, 100, 256, 512])
 def test_gemm_paths(gpu, scheme, m):
     _run(gpu, m, 320, 1024, scheme, seed=m)
     _run(gpu, m, 250, 640, scheme, seed=m + 9, bias=False)
 
 
-@pytest.mark.parametrize("m", [24, 70])
+@pytest.mark.parametrize("m", [24, 48, 70])
 def test_gemm_padded_k(gpu, m):
     # INT4 K = 904 pads to 1024: the last stage holds 8-column chunks past K.
     _run(gpu, m, 48, 904, "int4", seed=m + 3)
