@@ -1158,6 +1158,10 @@ constexpr int64_t kSkinnyLdsSmall = 64 * 1024;  // staging this small never limi
 constexpr int64_t kSkinnyLdsTwo = 80 * 1024;    // two workgroups per CU: LDS even over rounds
 constexpr int64_t kSkinnySplitMinM = 3;         // K split across workgroups from this M
 constexpr int64_t kSkinnySplitMinK = 8192;      // ... and this K
+// From this M the K split aims at two workgroups per CU (one below): down_proj
+// at M = 5 / 6 went 29.7 / 28.9 -> 20.2 / 20.4 us INT8, 23.9 / 22.2 -> 19.5 /
+// 19.8 us INT4 (5 -> 8 slices); at M = 3 / 4 INT4 loses 2 us.
+constexpr int64_t kSkinnySplit2MinM = 5;
 constexpr int64_t kCUs = 256;
 constexpr int kGemmWN = 4;                    // waves per workgroup (one column strip each)
 // 16-column tiles per wave: two (BN = 128) unless that gives more than
@@ -1260,7 +1264,8 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
         auto slice = [&](int64_t s) { return (p.nunits + s - 1) / s; };
         int64_t s = 1;
         while (s < p.nunits &&
-               (tiles4 * s < kCUs || 128 * ((slice(s) * tpu + 1) | 1) * m > kSkinnyLdsSmall))
+               (tiles4 * s < (m >= kSkinnySplit2MinM ? 2 : 1) * kCUs ||
+                128 * ((slice(s) * tpu + 1) | 1) * m > kSkinnyLdsSmall))
           ++s;
         if (s > 1) {
           p.nt = 4;

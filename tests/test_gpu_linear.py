@@ -90,6 +90,8 @@ def test_skinny_paths(gpu, scheme, m):
 
 @pytest.mark.parametrize("m,n,k,scheme", [
     (3, 4096, 14336, "int8"),    # down_proj at the split's smallest M
+    (5, 4096, 14336, "int8"),    # two workgroups per CU from M = 5: 8 slices
+    (6, 4096, 14336, "int4"),
     (4, 4096, 14336, "int4"),    # down_proj: 4 K slices of 28 groups
     (8, 4096, 14336, "int8"),    # 8 slices of 28 windows
     (16, 4096, 14336, "int4"),   # split rows (no hi / lo pairing), 16 slices
