@@ -1164,6 +1164,11 @@ constexpr int64_t kSkinnySplitMinK = 8192;      // ... and this K
 constexpr int64_t kSkinnySplit2MinM = 5;
 constexpr int64_t kCUs = 256;
 constexpr int kGemmWN = 4;                    // waves per workgroup (one column strip each)
+// INT8 on very wide N (the wide-tile case below, i.e. lm_head) runs 8 waves
+// of four tiles (BN = 512) with the two-per-CU split target (a 2-way K split
+// on [128256 x 4096]): measured 132.8 -> 119.4 us at M = 17, 140.5 -> 133.3
+// us at M = 32 (8 waves without the split: slower); INT4 loses there.
+constexpr int kGemmWideWN8 = 8;
 // 16-column tiles per wave: two (BN = 128) unless that gives more than
 // kGemmNarrowMaxTiles column tiles, then four (BN = 256).  Measured at M =
 // 17-32 on the Llama-3-8B shapes: BN = 128 takes 2-4 us off down / o /
@@ -1195,7 +1200,8 @@ struct Plan {
   int64_t nunits = 0;   // INT4 groups / INT8 windows per row
   int64_t nT = 0;       // k-steps
   int mtw = 0;          // gemm: 16-row m-tiles per wave (BM = 16 * mtw)
-  int ntw = 4;          // gemm: 16-column tiles per wave (BN = 16 * ntw * kGemmWN)
+  int ntw = 4;          // gemm: 16-column tiles per wave (BN = 16 * ntw * wn)
+  int wn = kGemmWN;     // gemm: waves per workgroup
   int64_t tiles_m = 0;  // gemm: workgroup tiles along M
   int64_t tiles_n = 0;  // gemm: workgroup tiles along N
   int64_t nstages = 0;  // gemm: 128-column K stages
@@ -1349,13 +1355,17 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
     const int64_t wide = (n + 64 * kWsWideNC - 1) / (64 * kWsWideNC);
     p.wsnc = bits == 4 && p.tiles_m * wide >= kWsWideMinTiles ? kWsWideNC : kWsNC;
   }
-  if (!p.wspec) p.ntw = (n + 16 * 2 * kGemmWN - 1) / (16 * 2 * kGemmWN) <= kGemmNarrowMaxTiles ? 2 : 4;
-  const int64_t bn = p.wspec ? 64 * p.wsnc : 16 * p.ntw * kGemmWN;
+  if (!p.wspec) {
+    p.ntw = (n + 16 * 2 * kGemmWN - 1) / (16 * 2 * kGemmWN) <= kGemmNarrowMaxTiles ? 2 : 4;
+    if (p.ntw == 4 && bits == 8 && p.mtw == 2) p.wn = kGemmWideWN8;
+  }
+  const int64_t bn = p.wspec ? 64 * p.wsnc : 16 * p.ntw * p.wn;
   p.tiles_n = (n + bn - 1) / bn;
   p.nstages = keff / 128;
   // Split K only as far as needed to give every CU two workgroups.
   const int64_t tiles = p.tiles_m * p.tiles_n;
-  const int64_t target = p.wspec ? kGemmWsTargetBlocks : (bits == 8 ? kGemmTargetBlocks8 : kGemmTargetBlocks);
+  const int64_t target = p.wspec ? kGemmWsTargetBlocks
+                                 : (bits == 8 && p.wn != kGemmWideWN8 ? kGemmTargetBlocks8 : kGemmTargetBlocks);
   int64_t s = 1;
   if (tiles < target)
     s = std::max<int64_t>(1, std::min(target / tiles, p.nstages / kGemmMinStages));
@@ -1492,12 +1502,12 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }
 
-template <int BITS, int MTW, int NTW>
+template <int BITS, int MTW, int NTW, int WN = kGemmWN>
 void launch_gemm_t(const Plan& p, const half8_t* planes, int64_t m, const uint8_t* wq,
                    const uint16_t* sc, int64_t row_bytes, int64_t ng, const float* bias, float* y,
                    int64_t ldy, int64_t n, float* part, hipStream_t st) {
   const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
-  gemm_kernel<BITS, MTW, NTW, kGemmWN><<<blocks, 64 * kGemmWN, 0, st>>>(
+  gemm_kernel<BITS, MTW, NTW, WN><<<blocks, 64 * WN, 0, st>>>(
       planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m, (int)p.tiles_n,
       p.gm, bias, y, ldy, n, part);
 }
@@ -1527,6 +1537,7 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
 #undef KQ_WS
   } else if (p.mtw == 2) {
     if (p.ntw == 2) launch_gemm_t<BITS, 2, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    else if (p.wn == kGemmWideWN8) launch_gemm_t<BITS, 2, 4, kGemmWideWN8>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
     else launch_gemm_t<BITS, 2, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   } else {
     if (p.ntw == 2) launch_gemm_t<BITS, 4, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
