@@ -61,6 +61,14 @@ SHAPES = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096)
 # q/k/v and gate/up row-stacked into one weight each: one launch per group.
 FUSED = [("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up", 28672, 4096),
          ("down_proj", 4096, 14336)]
+# Qwen2.5-0.5B decoder (24 layers, hidden 896, intermediate 4864, 14 / 2 heads
+# of 64): the small-model INT4 decode step, launch-bound by construction.
+QWEN_LAYERS = 24
+QWEN_SHAPES = [("q_proj", 896, 896), ("k_proj", 128, 896), ("v_proj", 128, 896),
+               ("o_proj", 896, 896), ("gate_proj", 4864, 896), ("up_proj", 4864, 896),
+               ("down_proj", 896, 4864)]
+QWEN_FUSED = [("qkv", 1152, 896), ("o_proj", 896, 896), ("gate_up", 9728, 896),
+              ("down_proj", 896, 4864)]
 
 
 def algorithmic_bytes(m, n, k, scheme):
@@ -90,14 +98,14 @@ class Proj:
         _lib.check(st)
 
 
-def build_layers(scheme, dev, seed, nlayers=LAYERS):
+def build_layers(scheme, dev, seed, nlayers=LAYERS, shapes=None):
     """``nlayers`` layers x 7 projections, N(0, 0.02) weights drawn on the GPU
     and quantized by the HIP kernel."""
     g = torch.Generator(device=dev).manual_seed(seed)
     layers = []
     for _ in range(nlayers):
         layer = {}
-        for name, n, k in SHAPES:
+        for name, n, k in shapes or SHAPES:
             w = torch.randn(n, k, device=dev, generator=g) * 0.02
             qw = quantize_int8_per_channel(w) if scheme == "int8" else quantize_int4_per_group(w, 128)
             del w
@@ -113,9 +121,9 @@ def build_layers(scheme, dev, seed, nlayers=LAYERS):
 class Sweep:
     """All launches of one decode step at batch M, with preallocated buffers."""
 
-    def __init__(self, layers, m, dev, names=None):
+    def __init__(self, layers, m, dev, names=None, shapes=None):
         self.names = names or [s[0] for s in SHAPES]
-        shapes = {s[0]: s for s in SHAPES + FUSED}
+        shapes = {s[0]: s for s in (shapes or SHAPES + FUSED)}
         self.calls = []
         lib = _lib.load()
         ws_bytes = 0
@@ -176,8 +184,8 @@ def time_steps(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps            # ms per step
 
 
-def measure(layers, m, dev, steps, warmup, eager, names=None):
-    sw = Sweep(layers, m, dev, names)
+def measure(layers, m, dev, steps, warmup, eager, names=None, shapes=None):
+    sw = Sweep(layers, m, dev, names, shapes)
     if not eager:
         sw.capture()
     ms = time_steps(sw.step, steps, warmup)
@@ -469,6 +477,13 @@ def main():
             r = measure(int8, 1, dev, args.steps, args.warmup, args.eager, names=[name])
             per8[name] = {"gbs": round(r["gbs"], 1), "us_per_launch": round(r["ms"] * 1e3 / nl, 2)}
         breakdown["int8_m1_per_projection"] = per8
+        qwen = build_layers("int4", dev, seed=5, nlayers=QWEN_LAYERS, shapes=QWEN_SHAPES)
+        rq = measure(qwen, 1, dev, args.steps, args.warmup, args.eager,
+                     names=[f[0] for f in QWEN_FUSED], shapes=QWEN_SHAPES + QWEN_FUSED)
+        breakdown["int4_m1_qwen2.5_0.5b_fused_step"] = {
+            "gbs": round(rq["gbs"], 1), "us_per_step": round(rq["ms"] * 1e3, 1),
+            "bytes_per_step": rq["bytes"], "launches": 4 * QWEN_LAYERS}
+        del qwen
         for m in (4, 8, 32, 64):
             r = measure(int8, m, dev, max(args.steps // 2, 3), 1, args.eager)
             breakdown[f"int8_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
