@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
-from typing import Dict, Tuple
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -107,17 +107,76 @@ def ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
 
-# Workspace buffers, one per (device, stream).  Calls on one stream are
-# ordered, so reusing the buffer across them is safe.
+# Workspace buffers.
+#
+# Eager calls: one buffer per (device, stream).  Calls on one stream are
+# ordered, so they can share it; when a call needs more, the buffer is
+# replaced and the old one returns to torch's caching allocator, whose reuse
+# of it is ordered on the same stream.
+#
+# Calls recorded into a HIP graph bake the buffer's address into the graph's
+# kernel nodes, and a replay writes there long after the call returned.  Such
+# calls therefore get buffers of their own, keyed by (device, stream, capture
+# id): shared only by calls of the same capture (ordered on its stream), never
+# by eager calls or other graphs, and never freed -- a buffer superseded
+# inside a capture is retired, not released -- until
+# ``release_graph_workspaces()`` is called once those graphs are gone.
 _ws: Dict[Tuple[int, int], torch.Tensor] = {}
+_graph_ws: Dict[Tuple[int, int, int], torch.Tensor] = {}
+_graph_retired: List[torch.Tensor] = []
+_MIN_WS = 1 << 20
 
 
-def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+def _alloc(device: torch.device, nbytes: int) -> torch.Tensor:
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+_hip = None
+
+
+def _capture_id(stream: int) -> Optional[int]:
+    """The id of the HIP graph capture ``stream`` is recording, or None."""
+    global _hip
+    if not torch.cuda.is_current_stream_capturing():
+        return None
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
+        _hip.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
+                                                 ctypes.POINTER(ctypes.c_ulonglong)]
+    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    err = _hip.hipStreamGetCaptureInfo(ctypes.c_void_p(stream), ctypes.byref(status),
+                                       ctypes.byref(cid))
+    if err != 0:
+        raise RuntimeError(f"kshipra_amd: hipStreamGetCaptureInfo failed ({err})")
+    return int(cid.value)
+
+
+def workspace(device: torch.device, stream: int, nbytes: int) -> Optional[torch.Tensor]:
     if nbytes == 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
-    buf = _ws.get(key)
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    cid = _capture_id(stream)
+    if cid is None:
+        key = (dev, stream)
+        buf = _ws.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = _alloc(device, max(nbytes, _MIN_WS))
+            _ws[key] = buf
+        return buf
+    gkey = (dev, stream, cid)
+    buf = _graph_ws.get(gkey)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _ws[key] = buf
+        if buf is not None:
+            _graph_retired.append(buf)        # captured kernels still point into it
+        buf = _alloc(device, max(nbytes, _MIN_WS))
+        _graph_ws[gkey] = buf
     return buf
+
+
+def release_graph_workspaces() -> None:
+    """Free every workspace handed to calls made under HIP graph capture.
+    Only safe once no graph that captured a call of this library will be
+    replayed again."""
+    _graph_ws.clear()
+    _graph_retired.clear()

@@ -4,8 +4,14 @@
   as the dict Kshipra's tests save (``torch.save({"payload": ..., "scales":
   ...})``, tests/test_quantization.py:312), plus the metadata a
   ``QuantizedWeight`` needs (``scheme``, ``original_shape``, ``group_size``,
-  ``in_features_padded``) so it loads back without the fp32 original.  Read
-  with ``torch.load(weights_only=True)``: nothing in the file is executed.
+  ``in_features_padded``) so it loads back without the fp32 original.
+  ``load_quantized`` also reads the reference's bare ``{"payload",
+  "scales"}`` dict: the scheme follows from the payload dtype (int8 ->
+  per-channel, uint8 -> packed INT4), the shape from the payload and the
+  INT4 group size from ``2 * payload columns / scale columns``; an INT4
+  weight whose ``in_features`` was padded needs ``in_features`` from the
+  caller (the padding is not recorded in that dict).  Read with
+  ``torch.load(weights_only=True)``: nothing in the file is executed.
 * ``save_quantized_weights(weights, path)`` / ``load_quantized_weights(path,
   device)``: a name -> ``QuantizedWeight`` mapping (a whole model's
   projections) as one safetensors file, tensors ``<name>.payload`` /
@@ -52,11 +58,55 @@ def save_quantized(qw: QuantizedWeight, path: str) -> None:
     torch.save(d, path)
 
 
-def load_quantized(path: str, device: Union[str, torch.device, None] = None) -> QuantizedWeight:
+def _infer_meta(payload: torch.Tensor, scales: torch.Tensor,
+                in_features: Optional[int], group_size: Optional[int]) -> dict:
+    """Metadata of a bare ``{"payload", "scales"}`` dict (the layouts of
+    engine/quantization.py:40-46)."""
+    if payload.dim() != 2:
+        raise QuantizationError(f"payload must be 2-D, got {tuple(payload.shape)}")
+    n, cols = payload.shape
+    if payload.dtype == torch.int8:
+        k = cols if in_features is None else int(in_features)
+        if k != cols:
+            raise QuantizationError(f"in_features {k} != INT8 payload columns {cols}")
+        return {"scheme": "int8_per_channel", "original_shape": [n, k], "group_size": None,
+                "in_features_padded": None}
+    if payload.dtype != torch.uint8:
+        raise QuantizationError(f"payload dtype {payload.dtype} is neither int8 nor uint8")
+    if scales.dim() != 2 or scales.shape[1] == 0:
+        raise QuantizationError(f"INT4 scales must be 2-D [out, groups], got {tuple(scales.shape)}")
+    kp = 2 * cols
+    if kp % scales.shape[1] != 0:
+        raise QuantizationError(f"{kp} padded columns do not split into {scales.shape[1]} groups")
+    g = kp // scales.shape[1]
+    if group_size is not None and int(group_size) != g:
+        raise QuantizationError(f"group_size {group_size} != {g} implied by the payload and scales")
+    k = kp if in_features is None else int(in_features)
+    if not (kp - g < k <= kp):
+        raise QuantizationError(f"in_features {k} is inconsistent with {kp} padded columns (G = {g})")
+    return {"scheme": "int4_per_group", "original_shape": [n, k], "group_size": g,
+            "in_features_padded": kp}
+
+
+def load_quantized(path: str, device: Union[str, torch.device, None] = None,
+                   in_features: Optional[int] = None,
+                   group_size: Optional[int] = None) -> QuantizedWeight:
+    """One ``QuantizedWeight`` from ``path``, its tensors placed on ``device``.
+
+    Files written by ``save_quantized`` carry their metadata; the reference's
+    bare ``{"payload", "scales"}`` dict has it inferred (``in_features`` /
+    ``group_size``, when given, are checked against it).
+    """
     d = torch.load(path, map_location=device if device is not None else "cpu", weights_only=True)
     if not isinstance(d, dict) or "payload" not in d or "scales" not in d:
         raise QuantizationError(f"{path}: not a quantized weight (expected payload and scales)")
-    return _build(d["payload"], d["scales"], d)
+    if any(key in d for key in _META_KEYS):
+        qw = _build(d["payload"], d["scales"], d)
+        if in_features is not None and int(in_features) != qw.original_shape[1]:
+            raise QuantizationError(f"in_features {in_features} != saved {qw.original_shape[1]}")
+        return qw
+    return _build(d["payload"], d["scales"], _infer_meta(d["payload"], d["scales"], in_features,
+                                                         group_size))
 
 
 def save_quantized_weights(weights: Dict[str, QuantizedWeight], path: str,

@@ -85,6 +85,46 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// DPP lane moves (gfx9 encodings of dpp_ctrl): quad permutations, the
+// half-row / row mirrors and the row broadcasts of lane 15 / 31.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move(float v) {
+  const int i = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <- 7 - i within 8
+constexpr int kDppMirror = 0x140;       // lane i <- 15 - i within 16
+constexpr int kDppBcast15 = 0x142;      // row r <- lane 15 of row r - 1
+constexpr int kDppBcast31 = 0x143;      // rows 2, 3 <- lane 31
+
+// Maximum over aligned groups of g lanes (g = 4, 8, 16, 32 or 64), returned
+// to every lane of the group.  Masked-off lanes keep their own value, which
+// leaves the maximum unchanged.
+__device__ __forceinline__ float group_max(float v, int g) {
+  v = __builtin_fmaxf(v, dpp_move<kDppXor1>(v));
+  v = __builtin_fmaxf(v, dpp_move<kDppXor2>(v));
+  if (g > 4) v = __builtin_fmaxf(v, dpp_move<kDppHalfMirror>(v));
+  if (g > 8) v = __builtin_fmaxf(v, dpp_move<kDppMirror>(v));
+  if (g > 16) v = __builtin_fmaxf(v, __shfl_xor(v, 16, 64));
+  if (g > 32) v = __builtin_fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+// Maximum over the whole wave as a wave-uniform value: reduce within rows of
+// 16, then carry row maxima upward with the row broadcasts; lane 63 ends with
+// the total.
+__device__ __forceinline__ float wave_max_uniform(float v) {
+  v = __builtin_fmaxf(v, dpp_move<kDppXor1>(v));
+  v = __builtin_fmaxf(v, dpp_move<kDppXor2>(v));
+  v = __builtin_fmaxf(v, dpp_move<kDppHalfMirror>(v));
+  v = __builtin_fmaxf(v, dpp_move<kDppMirror>(v));
+  v = __builtin_fmaxf(v, dpp_move<kDppBcast15, 0xa>(v));
+  v = __builtin_fmaxf(v, dpp_move<kDppBcast31, 0xc>(v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ __forceinline__ int wave_or(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
@@ -157,7 +197,8 @@ __host__ __device__ constexpr int perm_int8(int s) {
 // so a lane's 16-byte weight load (INT4: one quarter of a 128-column group;
 // INT8: one quarter of a 64-column window) feeds 4 (INT4) or 2 (INT8)
 // consecutive k-steps.  The activation operand uses the same map; it is
-// staged as fp16 hi/lo pairs (x = hi + lo, hi = fp16(x), lo = fp16(x - hi)).
+// staged as fp16 hi/lo pairs of the power-of-two scaled activation
+// (x 2^e = hi + lo, hi = fp16(x 2^e), lo = fp16(x 2^e - hi); see below).
 // ---------------------------------------------------------------------------
 template <int BITS>
 __host__ __device__ constexpr int64_t kstep_col0(int64_t T, int qd) {
@@ -173,12 +214,51 @@ __device__ __forceinline__ floatx4 mfma16x16x32(half8_t a, half8_t b, floatx4 c)
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Split 8 fp32 activations (already in slot order) into fp16 hi/lo halves.
-__device__ __forceinline__ void split_hi_lo(const float (&v)[8], half8_t& hi, half8_t& lo) {
+// ---------------------------------------------------------------------------
+// Range-safe activation split.
+//
+// fp16 covers 2^-24 .. 65504; fp32 activations span 2^-149 .. 2^128.  A row
+// of x (or the K-slice of a row that one accumulation chain covers) is
+// therefore scaled by an exact power of two 2^e, chosen from its largest
+// magnitude so that max |x| * 2^e lies in [2^14, 2^15), before it is split
+// into hi = fp16(x 2^e) and lo = fp16(x 2^e - hi).  The products of exact
+// fp16 weights with hi / lo are exact in the fp32 accumulators, and the sum
+// is scaled back by 2^-e (exact unless the result itself leaves the fp32
+// range).  The representation error of an element is at most 2^-22 |x| (hi
+// keeps 11 bits, lo the next 11) plus 2^-25 in the scaled domain (lo's
+// subnormal spacing), i.e. 2^-39 of the slice maximum: fp32-class for every
+// finite x, whatever its magnitude.
+//
+// Non-finite entries: the maximum is taken over |x| with NaN ignored and is
+// clamped to FLT_MAX, so a row holding +-inf keeps its finite entries in
+// range; +-inf itself becomes hi = +-inf, lo = 0 (products inf * q give +-inf,
+// or NaN for q = 0, as the fp32 product does); NaN stays NaN.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float absmax8(const float (&v)[8], float m) {
+#pragma unroll
+  for (int s = 0; s < 8; s++) m = __builtin_fmaxf(m, __builtin_fabsf(v[s]));
+  return m;
+}
+
+// Scale exponent of a row-slice whose largest magnitude is amax (>= 0):
+// amax * 2^e in [2^14, 2^15); 0 for an all-zero (or all-NaN) slice.
+__device__ __forceinline__ int act_exponent(float amax) {
+  amax = __builtin_fminf(amax, 3.40282347e38f);
+  return amax > 0.0f ? 15 - __builtin_amdgcn_frexp_expf(amax) : 0;
+}
+
+// Split 8 fp32 activations (already in slot order) scaled by 2^e into fp16
+// hi/lo halves.
+__device__ __forceinline__ void split_hi_lo(const float (&v)[8], int e, half8_t& hi, half8_t& lo) {
 #pragma unroll
   for (int s = 0; s < 8; s++) {
-    _Float16 h = (_Float16)v[s];
+    const float t = __builtin_amdgcn_ldexpf(v[s], e);
+    const _Float16 h = (_Float16)t;
+    const float d = t - (float)h;
     hi[s] = h;
-    lo[s] = (_Float16)(v[s] - (float)h);
+    lo[s] = (_Float16)(d == d ? d : 0.0f);   // +-inf: inf - inf = NaN -> 0
   }
 }
+
+// Undo the activation scale on an fp32 (partial) sum.
+__device__ __forceinline__ float unscale(float v, int e) { return __builtin_amdgcn_ldexpf(v, -e); }

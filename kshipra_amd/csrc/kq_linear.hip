@@ -12,14 +12,16 @@
 //    partial sum; INT8 row scales scale the final sum.  The waves of a
 //    workgroup split K and are reduced through LDS in a fixed order
 //    (deterministic).  The activations are staged as fp16 hi/lo MFMA operands
-//    in LDS by the workgroup itself when they fit, else by stage_skinny_kernel into
-//    the caller's workspace.
+//    in LDS by the workgroup itself when they fit (each wave scales its own
+//    K-slice of a row), else by stage_rows_kernel into the caller's
+//    workspace (one scale per row).
 //  * gemm_kernel    (17 <= M <= 32, batched decode): workgroup tile BM x 128
 //    (x 256 for very wide N); x is converted once per call into fp16 hi/lo operand planes
-//    (stage_planes_kernel), each 128-column stage of them is copied into LDS
+//    (stage_rows_kernel), each 128-column stage of them is copied into LDS
 //    (double-buffered) and shared by the waves; each wave streams its own
 //    weight columns from HBM into registers one stage ahead.  K is split across workgroups when the tiles alone cannot
 //    fill the GPU; partials are then added in a fixed order.
+//  * gemm_ws_kernel (prefill chunks): warp-specialised variant fed by DMA.
 //  * generic_kernel (any group size / K): scalar dequant + FMA fallback for
 //    shapes the MFMA paths do not tile.
 #include <algorithm>
@@ -30,7 +32,10 @@ namespace {
 
 // ---------------------------------------------------------------------------
 // Activation staging.  An "entry" (T, qd, m) is the 8 activations of row m that
-// lane quad qd feeds to k-step T, split into fp16 hi and lo halves.
+// lane quad qd feeds to k-step T, scaled by the power of two 2^e of its row
+// (or row-slice; kq_common.hpp) and split into fp16 hi and lo halves.  Every
+// sum over staged entries is scaled back by 2^-e before it leaves the
+// kernel (partials included).
 //
 // Skinny layout (lane-major, one array): A-row r, quad qd, k-step T at
 //   index (qd * R + r) * pitch + T,   a lane's k-steps 16 bytes apart.
@@ -38,7 +43,7 @@ namespace {
 //     The MFMA sees hi and lo as different A rows, so one MFMA per k-step
 //     yields both partial sums (rows m and m + 8 of the output tile).
 //   split mode (M <= 16): R = M rows in two arrays (hi, lo); two MFMAs per k-step.
-// GEMM operand planes: see stage_planes_kernel.
+// GEMM operand planes: see stage_rows_kernel.
 // ---------------------------------------------------------------------------
 // Load the 8 consecutive activations of entry (T, qd, m) (zeros past M / K).
 template <int BITS>
@@ -63,52 +68,147 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, int64_t 
   }
 }
 
-// Permute the 8 loaded activations into operand-slot order and split them.
+// Permute the 8 loaded activations into operand-slot order, scale them by
+// 2^e and split them.
 template <int BITS>
-__device__ __forceinline__ void stage_convert(const float (&raw8)[8], half8_t& hi, half8_t& lo) {
+__device__ __forceinline__ void stage_convert(const float (&raw8)[8], int e, half8_t& hi, half8_t& lo) {
   float v[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) v[s] = raw8[kstep_perm<BITS>(s)];
-  split_hi_lo(v, hi, lo);
+  split_hi_lo(v, e, hi, lo);
 }
 
-template <int BITS>
-__device__ __forceinline__ void stage_entry(const float* __restrict__ x, int64_t ldx, int64_t M,
-                                            int64_t K, int T, int qd, int64_t m, bool xvec,
-                                            half8_t& hi, half8_t& lo) {
-  float raw8[8];
-  stage_load<BITS>(x, ldx, M, K, T, qd, m, xvec, raw8);
-  stage_convert<BITS>(raw8, hi, lo);
+// Skinny layout: the two 16-byte slots of entry (T, qd, m).  HL: one array,
+// rows m and M + m; split: the hi array, then the lo array.
+template <bool HL>
+__device__ __forceinline__ void skinny_slots(int M, int64_t pitch, int T, int qd, int m,
+                                             int64_t& ihi, int64_t& ilo) {
+  if constexpr (HL) {
+    ihi = (int64_t)(qd * 2 * M + m) * pitch + T;
+    ilo = (int64_t)(qd * 2 * M + M + m) * pitch + T;
+  } else {
+    ihi = (int64_t)(qd * M + m) * pitch + T;
+    ilo = (int64_t)4 * M * pitch + ihi;
+  }
 }
 
-// Skinny layout: write entry (T, qd, m).  HL: one array, rows m and M + m.
 template <bool HL>
 __device__ __forceinline__ void skinny_store(half8_t* __restrict__ a, int M, int64_t pitch,
                                              int T, int qd, int m, half8_t hi, half8_t lo) {
-  if constexpr (HL) {
-    a[(int64_t)(qd * 2 * M + m) * pitch + T] = hi;
-    a[(int64_t)(qd * 2 * M + M + m) * pitch + T] = lo;
+  int64_t ihi, ilo;
+  skinny_slots<HL>(M, pitch, T, qd, m, ihi, ilo);
+  a[ihi] = hi;
+  a[ilo] = lo;
+}
+
+// The raw fp32 values of an entry parked in its own two slots (32 bytes, the
+// size of the hi / lo pair) until the slice's scale is known.
+template <bool HL>
+__device__ __forceinline__ void skinny_park(half8_t* __restrict__ a, int M, int64_t pitch, int T,
+                                            int qd, int m, const float (&raw8)[8]) {
+  int64_t ihi, ilo;
+  skinny_slots<HL>(M, pitch, T, qd, m, ihi, ilo);
+  reinterpret_cast<floatx4*>(a)[ihi] = floatx4{raw8[0], raw8[1], raw8[2], raw8[3]};
+  reinterpret_cast<floatx4*>(a)[ilo] = floatx4{raw8[4], raw8[5], raw8[6], raw8[7]};
+}
+
+template <bool HL>
+__device__ __forceinline__ void skinny_unpark(const half8_t* __restrict__ a, int M, int64_t pitch,
+                                              int T, int qd, int m, float (&raw8)[8]) {
+  int64_t ihi, ilo;
+  skinny_slots<HL>(M, pitch, T, qd, m, ihi, ilo);
+  const floatx4 u = reinterpret_cast<const floatx4*>(a)[ihi];
+  const floatx4 v = reinterpret_cast<const floatx4*>(a)[ilo];
+#pragma unroll
+  for (int s = 0; s < 4; s++) { raw8[s] = u[s]; raw8[4 + s] = v[s]; }
+}
+
+// Largest |x| of the rows a workgroup of 64 * W threads stages (one value per
+// thread in, the workgroup maximum out; red holds W floats).
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max_uniform(v);
+  const int nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = red[0];
+  for (int w = 1; w < nw; w++) v = __builtin_fmaxf(v, red[w]);
+  return v;
+}
+
+// Stage whole activation rows, one workgroup per row m: the row's scale
+// exponent e (written to rexp[m]) from its largest |x|, then every entry
+// (T, qd) of the row converted with it.  Rows past M are zeros with e = 0.
+//   PLANES = false: skinny layout (HL or split), `pitch` entries per A-row.
+//   PLANES = true:  GEMM operand planes: entry (plane p, stage st, row m, e)
+//                   at ((p * nstages + st) * Mp + m) * 16 + e, e = (T % 4) * 4 + qd,
+//                   st = T / 4 (nT = 4 * nstages, gridDim.x = Mp).
+// A thread holds up to kStageHold entries in registers between the maximum
+// and the conversion; longer rows are read twice (the second read hits L2).
+constexpr int kStageHold = 8;
+template <int BITS, bool PLANES, bool HL>
+__global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict__ x, int64_t ldx,
+                                                         int M, int64_t K, int nT, int64_t pitch,
+                                                         int64_t Mp, bool xvec,
+                                                         half8_t* __restrict__ a,
+                                                         int* __restrict__ rexp) {
+  __shared__ float red[4];
+  const int m = blockIdx.x;
+  const int64_t E = (int64_t)nT * 4;
+  auto store = [&](int64_t q, half8_t hi, half8_t lo) {
+    const int T = (int)(q >> 2), qd = (int)(q & 3);
+    if constexpr (PLANES) {
+      const int64_t o = ((int64_t)(T >> 2) * Mp + m) * 16 + (T & 3) * 4 + qd;
+      const int64_t total = (int64_t)(nT >> 2) * Mp * 16;
+      a[o] = hi;
+      a[total + o] = lo;
+    } else {
+      skinny_store<HL>(a, M, pitch, T, qd, m, hi, lo);
+    }
+  };
+  float amax = 0.0f;
+  if (E <= (int64_t)kStageHold * blockDim.x) {
+    float raw[kStageHold][8];
+#pragma unroll
+    for (int j = 0; j < kStageHold; j++) {
+      const int64_t q = threadIdx.x + (int64_t)j * blockDim.x;
+      stage_load<BITS>(x, ldx, M, K, (int)(q >> 2), (int)(q & 3), q < E ? m : M, xvec, raw[j]);
+      amax = absmax8(raw[j], amax);
+    }
+    const int e = act_exponent(block_max(amax, red));
+#pragma unroll
+    for (int j = 0; j < kStageHold; j++) {
+      const int64_t q = threadIdx.x + (int64_t)j * blockDim.x;
+      if (q < E) {
+        half8_t hi, lo;
+        stage_convert<BITS>(raw[j], e, hi, lo);
+        store(q, hi, lo);
+      }
+    }
+    if (threadIdx.x == 0) rexp[m] = e;
   } else {
-    a[(int64_t)(qd * M + m) * pitch + T] = hi;
-    a[(int64_t)4 * M * pitch + (int64_t)(qd * M + m) * pitch + T] = lo;
+    for (int64_t q = threadIdx.x; q < E; q += blockDim.x) {
+      float raw[8];
+      stage_load<BITS>(x, ldx, M, K, (int)(q >> 2), (int)(q & 3), m, xvec, raw);
+      amax = absmax8(raw, amax);
+    }
+    const int e = act_exponent(block_max(amax, red));
+    for (int64_t q = threadIdx.x; q < E; q += blockDim.x) {
+      float raw[8];
+      stage_load<BITS>(x, ldx, M, K, (int)(q >> 2), (int)(q & 3), m, xvec, raw);
+      half8_t hi, lo;
+      stage_convert<BITS>(raw, e, hi, lo);
+      store(q, hi, lo);
+    }
+    if (threadIdx.x == 0) rexp[m] = e;
   }
 }
 
-template <int BITS, bool HL>
-__global__ __launch_bounds__(256) void stage_skinny_kernel(const float* __restrict__ x,
-                                                           int64_t ldx, int M, int64_t K,
-                                                           int nT, int64_t pitch, bool xvec,
-                                                           half8_t* __restrict__ a) {
-  const int64_t total = (int64_t)nT * 4 * M;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int T = (int)(e % nT);
-    const int r = (int)(e / nT);
-    const int m = r % M, qd = r / M;
-    half8_t hi, lo;
-    stage_entry<BITS>(x, ldx, M, K, T, qd, m, xvec, hi, lo);
-    skinny_store<HL>(a, M, pitch, T, qd, m, hi, lo);
-  }
+// Lanes per activation row in the skinny kernel's in-workgroup staging: 64
+// over M rounded up to a power of two (M <= 16: at least 4).
+__host__ __device__ inline int skinny_lanes_per_row(int M) {
+  int p = 1;
+  while (p < M) p <<= 1;
+  return 64 / p;
 }
 
 // Group scales of units [u0, u0 + KS) of one row.  SVEC: one vector load of
@@ -197,8 +297,10 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M_, int64_t K, bool xvec,
     const uint8_t* wq, const uint16_t* sc, int64_t row_bytes,
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
-    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
-    int2* __restrict__ argp, int pairs, int64_t split_units, int64_t split_ystride) {
+    const int* __restrict__ xexp, const float* __restrict__ bias, float* __restrict__ y,
+    int64_t ldy, int64_t N,
+    int2* __restrict__ argp, int pairs, int64_t split_units, int64_t split_ystride,
+    int* __restrict__ pexp) {
   static_assert(!M1 || (A_LDS && HL && !REM), "single-row instances stage in LDS, pre-loads only");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int TPU = BITS == 4 ? 4 : 2;  // k-steps per unit
@@ -243,44 +345,38 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
   // weights.  Then the first chunk of packed weights (and, for INT4, its group
   // scales) goes in flight, then the staging converts while HBM answers.
   // Each wave stages only the k-steps of its own units, [ub, ue) * TPU, so a
-  // wave-level sync replaces a workgroup barrier.  Entries are numbered
-  // f = m * E + e over the M rows (e: k-step tb + e / 4, quad e % 4); lane l
-  // owns f = l + 64 j.  The first pre_n <= PRE of them (every row) are loaded
-  // before the weights; only entries past them (or unaligned / K-tail x) are
-  // loaded after the weights, where converting them waits for the weights.
-  // One row: PRE covers one batch of KS units, loaded unconditionally.
+  // wave-level sync replaces a workgroup barrier.  Lane l stages activation
+  // row my_m = l / lpr (lpr = 64 / M rounded up to a power of two lanes per
+  // row) and its entries e = l % lpr + lpr j < E (k-step tb + e / 4, quad
+  // e % 4), so the lanes of a row are one aligned group and the row's scale
+  // (its largest |x| over this wave's K-slice) is a reduction within the
+  // group.  Slots j < pre_n <= PRE are loaded before the weights; entries past
+  // them (or unaligned / K-tail x) are loaded after the weights, where their
+  // conversion waits for the weights.  One row: PRE covers one batch of KS
+  // units, loaded unconditionally.
   constexpr int PRE1 = KS * TPU / 16 < 1 ? 1 : (KS * TPU / 16 > 4 ? 4 : KS * TPU / 16);
   constexpr int PRE = M1 ? PRE1 : 4;
   const int tb = (int)(ub * TPU), te = (int)(ue * TPU);
   const int E = (te - tb) * 4;
-  const int ntot = M * E;
-  const int pre_n = M1 ? PRE : ((ntot + 63) / 64 < PRE ? (ntot + 63) / 64 : PRE);
+  const int lpr = M1 ? 64 : skinny_lanes_per_row(M);
+  const int my_m = M1 ? 0 : lane / lpr;
+  const int sub = M1 ? lane : lane & (lpr - 1);
+  const bool row_lane = my_m < M;
+  const int per_lane = (E + lpr - 1) / lpr;
+  const int pre_n = M1 ? PRE : (per_lane < PRE ? per_lane : PRE);
   floatx4 xa4[PRE], xb4[PRE];
-  unsigned pre_mask = 0;  // bit j: entry lane + 64 j was pre-loaded
-  int pm[PRE], pe[PRE];   // its row and in-row index
+  unsigned pre_mask = 0;  // bit j: slot j was pre-loaded
   if constexpr (A_LDS) {
-    // (row, in-row index) of f = lane + 64 j, stepped without a division.
-    int m = 0, e = lane;
-#pragma unroll
-    for (int j = 0; j < PRE; j++) {
-      if (j > 0) e += 64;
-      if constexpr (!M1) {
-        while (e >= E && m < M) { e -= E; m++; }
-      }
-      pm[j] = m;
-      pe[j] = e;
-    }
 #pragma unroll
     for (int j = 0; j < PRE; j++) {
       if (M1 || j < pre_n) {
-        const int f = lane + 64 * j;
-        const int m = pm[j], e = pe[j];
+        const int e = sub + lpr * j;
         const int T = tb + (e >> 2), q4 = e & 3;
-        const bool ok = xvec && f < ntot && kstep_col0<BITS>(T, q4) + 8 <= K;
+        const bool ok = row_lane && xvec && e < E && kstep_col0<BITS>(T, q4) + 8 <= K;
         pre_mask |= (unsigned)ok << j;
-        // A skipped entry reads 32 bytes of the payload instead (rows are at
+        // A skipped slot reads 32 bytes of the payload instead (rows are at
         // least 64 bytes; x may hold fewer than 8 values).
-        const float* src = ok ? x + m * ldx + kstep_col0<BITS>(T, q4) : reinterpret_cast<const float*>(wq);
+        const float* src = ok ? x + my_m * ldx + kstep_col0<BITS>(T, q4) : reinterpret_cast<const float*>(wq);
         xa4[j] = reinterpret_cast<const floatx4*>(src)[0];
         xb4[j] = reinterpret_cast<const floatx4*>(src)[1];
       }
@@ -322,48 +418,92 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
   __builtin_amdgcn_sched_barrier(0);
 
   const half8_t* a = xa;
+  int ex = 0;  // this lane's row scale exponent (A_LDS staging)
   if constexpr (A_LDS) {
     half8_t* la = reinterpret_cast<half8_t*>(smem);
-    // A lane without a valid pre-load writes its (unused) values to the pad
-    // column T = nT of row 0, which no lane reads.
+    float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < PRE; j++) {
-      if (M1 || j < pre_n) {
-        const int m = pm[j], e = pe[j];
-        const bool ok = (pre_mask >> j) & 1;
+      if ((M1 || j < pre_n) && ((pre_mask >> j) & 1)) {
         const float raw8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
                                xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
-        half8_t hi, lo;
-        stage_convert<BITS>(raw8, hi, lo);
-        skinny_store<HL>(la, M, pitch, ok ? tb + (e >> 2) : nT, e & 3, ok ? m : 0, hi, lo);
+        amax = absmax8(raw8, amax);
       }
     }
-    // Everything else: four entries per lane at a time, their loads issued
-    // together so the latencies overlap.  Skipped (wave-uniformly) when the
-    // pre-loads covered every entry, so no wait for the weights is emitted.
-    // (K short of the units' columns: the pre-loads skipped the K-tail
-    // entries, which are staged here with zeros past K.)
-    if (REM && (ntot > 64 * pre_n || !xvec || K != nunits * (BITS == 4 ? 128 : 64))) {
-      for (int j0 = 0; 64 * j0 < ntot; j0 += 4) {
+    // The row's largest |x| over this wave's slice: the lpr lanes of a row
+    // are an aligned group of lanes.
+    auto row_exponent = [&](float v) {
+      if constexpr (M1) {
+        // one row: the exponent is wave-uniform (kept in a scalar register)
+        return __builtin_amdgcn_readfirstlane(act_exponent(wave_max_uniform(v)));
+      } else {
+        return act_exponent(lpr == 64 ? wave_max_uniform(v) : group_max(v, lpr));
+      }
+    };
+    if constexpr (!REM) {
+      // The pre-loads cover every entry: convert them from registers.  A slot
+      // without a valid pre-load writes its (unused) values to the pad
+      // column T = nT of row 0, which no lane reads.
+      ex = row_exponent(amax);
+#pragma unroll
+      for (int j = 0; j < PRE; j++) {
+        if (M1 || j < pre_n) {
+          const int e = sub + lpr * j;
+          const bool ok = (pre_mask >> j) & 1;
+          const float raw8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
+                                 xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
+          half8_t hi, lo;
+          stage_convert<BITS>(raw8, ex, hi, lo);
+          skinny_store<HL>(la, M, pitch, ok ? tb + (e >> 2) : nT, e & 3, ok ? my_m : 0, hi, lo);
+        }
+      }
+    } else {
+      // Every entry is parked raw in its own two LDS slots (32 bytes, the
+      // size of its hi / lo pair) until the row's scale is known: first the
+      // pre-loaded ones (freeing their registers), then the rest, loaded four
+      // slots per lane at a time with their loads issued together so the
+      // latencies overlap.  These loads come after the weights, so their use
+      // waits for the first weight batch.  (K short of the units' columns:
+      // the pre-loads skipped the K-tail entries, which are staged here with
+      // zeros past K.)  Each lane later reads back only what it parked.
+#pragma unroll
+      for (int j = 0; j < PRE; j++) {
+        if (j < pre_n && ((pre_mask >> j) & 1)) {
+          const int e = sub + lpr * j;
+          const float raw8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
+                                 xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
+          skinny_park<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, raw8);
+        }
+      }
+      for (int j0 = 0; j0 < per_lane; j0 += 4) {
         float raw8[4][8];
         bool need[4];
-        int mm[4], ee[4];
+        int ee[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const int j = j0 + r, f = lane + 64 * j;
-          need[r] = f < ntot && !(j < pre_n && ((pre_mask >> j) & 1));
-          mm[r] = need[r] ? f / E : 0;
-          ee[r] = need[r] ? f - mm[r] * E : 0;
+          const int j = j0 + r;
+          ee[r] = sub + lpr * j;
+          need[r] = row_lane && ee[r] < E && !(j < pre_n && ((pre_mask >> j) & 1));
           // row M: stage_load returns zeros without reading
-          stage_load<BITS>(x, ldx, M, K, tb + (ee[r] >> 2), ee[r] & 3, need[r] ? mm[r] : M, xvec, raw8[r]);
+          stage_load<BITS>(x, ldx, M, K, tb + (ee[r] >> 2), ee[r] & 3, need[r] ? my_m : M, xvec, raw8[r]);
         }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           if (need[r]) {
-            half8_t hi, lo;
-            stage_convert<BITS>(raw8[r], hi, lo);
-            skinny_store<HL>(la, M, pitch, tb + (ee[r] >> 2), ee[r] & 3, mm[r], hi, lo);
+            amax = absmax8(raw8[r], amax);
+            skinny_park<HL>(la, M, pitch, tb + (ee[r] >> 2), ee[r] & 3, my_m, raw8[r]);
           }
+        }
+      }
+      ex = row_exponent(amax);
+      for (int j = 0; j < per_lane; j++) {
+        const int e = sub + lpr * j;
+        if (row_lane && e < E) {
+          float raw8[8];
+          skinny_unpark<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, raw8);
+          half8_t hi, lo;
+          stage_convert<BITS>(raw8, ex, hi, lo);
+          skinny_store<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, hi, lo);
         }
       }
     }
@@ -452,32 +592,61 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 
   // Cross-wave reduction in a fixed order.  Lane (qd, c) holds output-tile
   // rows 4qd+i, column c of each tile (HL: row m is the hi part of x[m], row
-  // m + 8 its lo part).
-  __syncthreads();
+  // m + 8 its lo part), in its wave's scaled domain: 2^e_w[m] times the true
+  // sum, e_w[m] the wave's exponent of row m (staged in LDS: held by the
+  // lanes of row m; staged by the pre-pass: one exponent per row, xexp).
+  // The waves' sums of a row meet in the domain of the row's smallest
+  // exponent E (each term scaled by 2^(E - e_w) <= 1, exact unless it is
+  // negligible) and are scaled back by 2^-E once, so an output in the fp32
+  // subnormal range is rounded once.  With a K split the slice writes its
+  // sum still scaled, with E in pexp[slice * M + m], for the ordered
+  // reduction to combine.
   float* red = reinterpret_cast<float*>(smem);
+  int* sh_e;
+  {
+    const int red_bytes = nwaves * NT * 256 * 4;
+    const int stage_bytes = A_LDS ? 128 * pitch * M : 0;
+    sh_e = reinterpret_cast<int*>(smem + (red_bytes > stage_bytes ? red_bytes : stage_bytes));
+  }
+  if constexpr (A_LDS) {
+    if (sub == 0 && row_lane) sh_e[wave * 16 + my_m] = ex;
+  } else {
+    if (lane < M) sh_e[wave * 16 + lane] = xexp[lane];
+  }
+  __syncthreads();
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll
     for (int i = 0; i < 4; i++) red[((wave * NT + t) * 16 + 4 * qd + i) * 16 + c] = acc[t][i];
   __syncthreads();
+  const bool split = !M1 && gridDim.y > 1;
+  // Row m's common exponent and the sum over waves of tile t, column cc.
+  auto row_exp = [&](int m) {
+    int e = sh_e[m];
+    for (int w = 1; w < nwaves; w++) e = min(e, sh_e[w * 16 + m]);
+    return e;
+  };
+  auto wave_sum = [&](int t, int m, int cc, int e) {
+    float v = 0.0f;
+    for (int w = 0; w < nwaves; w++) {
+      const int d = e - sh_e[w * 16 + m];
+      v += __builtin_amdgcn_ldexpf(red[((w * NT + t) * 16 + m) * 16 + cc], d);
+      if constexpr (HL) v += __builtin_amdgcn_ldexpf(red[((w * NT + t) * 16 + m + 8) * 16 + cc], d);
+    }
+    return v;
+  };
   // Gate / up pairs (NT == 2, weights interleaved by 16-row tiles): tile 0
   // holds gate rows, tile 1 the up rows of the same 16 output columns;
-  // y[m][16 b + c] = silu(g) * up.
+  // y[m][16 b + c] = silu(g) * up.  (Never K-split.)
   if constexpr (NT == 2) {
     if (pairs) {
       for (int o = tid; o < M * 16; o += blockDim.x) {
         const int m = o >> 4, cc = o & 15;
         const int64_t ngate = ncol0 + cc, nup = ngate + 16;
         if (nup < N) {
-          float g = 0.0f, u = 0.0f;
-          for (int w = 0; w < nwaves; w++) {
-            g += red[((w * NT) * 16 + m) * 16 + cc];
-            u += red[((w * NT + 1) * 16 + m) * 16 + cc];
-            if constexpr (HL) {
-              g += red[((w * NT) * 16 + m + 8) * 16 + cc];
-              u += red[((w * NT + 1) * 16 + m + 8) * 16 + cc];
-            }
-          }
+          const int e = row_exp(m);
+          float g = unscale(wave_sum(0, m, cc, e), e);
+          float u = unscale(wave_sum(1, m, cc, e), e);
           if constexpr (BITS == 8) { g *= f16_bits_to_f32(sc[ngate]); u *= f16_bits_to_f32(sc[nup]); }
           if (bias) { g += bias[ngate]; u += bias[nup]; }
           y[m * ldy + (int64_t)blockIdx.x * 16 + cc] = g / (1.0f + expf(-g)) * u;
@@ -496,11 +665,15 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     float v = -__builtin_inff();
     int vi = 0x7fffffff;
     if (nn < N) {
-      v = 0.0f;
-      for (int w = 0; w < nwaves; w++) {
-        v += red[((w * NT + t) * 16 + m) * 16 + cc];
-        if constexpr (HL) v += red[((w * NT + t) * 16 + m + 8) * 16 + cc];
+      const int e = row_exp(m);
+      v = wave_sum(t, m, cc, e);
+      if (split) {
+        if constexpr (BITS == 8) v *= f16_bits_to_f32(sc[nn]);
+        y[m * ldy + nn] = v;                       // partial, still scaled by 2^e
+        if (nn == ncol0) pexp[(int64_t)blockIdx.y * M + m] = e;
+        continue;
       }
+      v = unscale(v, e);
       if constexpr (BITS == 8) v *= f16_bits_to_f32(sc[nn]);
       if (bias) v += bias[nn];
       if (y) y[m * ldy + nn] = v;
@@ -540,13 +713,14 @@ __device__ __forceinline__ void gemm_tile(int tiles_m, int tiles_n, int gm, int6
 // ---------------------------------------------------------------------------
 // GEMM path: M > 16 (batched decode, prefill chunks).
 //
-// stage_planes_kernel converts x once per call into fp16 hi/lo MFMA operand
+// stage_rows_kernel converts x once per call into fp16 hi/lo MFMA operand
 // planes in the workspace:  entry (plane p, stage st, row m, e) at
 //   ((p * nstages + st) * Mp + m) * 16 + e        (16-byte units)
 // where stage st covers K columns [128 st, 128 st + 128), e = T * 4 + qd names
 // the 8 columns lane quad qd feeds to k-step T of the stage (already permuted
 // into operand-slot order), Mp is M rounded up to the row tile, and rows past
-// M / columns past K are zeros.
+// M / columns past K are zeros.  Row m is scaled by 2^rexp[m]; the epilogues
+// scale the sums back.
 //
 // gemm_kernel: workgroup = WN waves side by side along N; wave tile 16*MTW
 // rows x 16*NTW columns, so the workgroup tile is BM = 16*MTW by
@@ -566,31 +740,13 @@ __device__ __forceinline__ void gemm_tile(int tiles_m, int tiles_n, int gm, int6
 // it writes fp32 partials and splitk_reduce_kernel adds them in z order
 // (deterministic).
 // ---------------------------------------------------------------------------
-template <int BITS>
-__global__ __launch_bounds__(256) void stage_planes_kernel(const float* __restrict__ x, int64_t ldx,
-                                                           int64_t M, int64_t K, int64_t nstages,
-                                                           int64_t Mp, bool xvec,
-                                                           half8_t* __restrict__ planes) {
-  const int64_t total = nstages * Mp * 16;
-  for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
-       o += (int64_t)gridDim.x * blockDim.x) {
-    const int e = (int)(o & 15);
-    const int64_t r = o >> 4;
-    const int64_t m = r % Mp, st = r / Mp;
-    half8_t hi, lo;
-    stage_entry<BITS>(x, ldx, M, K, (int)(st * 4 + (e >> 2)), e & 3, m, xvec, hi, lo);
-    planes[o] = hi;
-    planes[total + o] = lo;
-  }
-}
-
 template <int BITS, int MTW, int NTW, int WN>
 __global__ __launch_bounds__(64 * WN) void gemm_kernel(
     const half8_t* __restrict__ planes, int64_t Mp, int64_t M,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
     int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n, int gm,
-    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
-    float* __restrict__ part) {
+    const int* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y,
+    int64_t ldy, int64_t N, float* __restrict__ part) {
   constexpr int BM = 16 * MTW;
   constexpr int NTHR = 64 * WN;
   constexpr int PLANE = BM * 16;           // LDS entries per plane
@@ -736,7 +892,14 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
   }
   if (st < se) stage(st, 0, wa, sa, wb, sbv);  // odd stage count
 
-  // Lane (qd, c) holds rows 16*mt + 4*qd + i, column 16*t + c of its wave tile.
+  // Lane (qd, c) holds rows 16*mt + 4*qd + i, column 16*t + c of its wave
+  // tile; each row is scaled back by its activation exponent (rows past M
+  // are padding: exponent 0 in the planes' padded rows).
+  int er[MTW][4];
+#pragma unroll
+  for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) er[mt][i] = rexp[m0 + mt * 16 + 4 * qd + i];
 #pragma unroll
   for (int t = 0; t < NTW; t++) {
     const int64_t n = n0 + t * 16 + c;
@@ -753,8 +916,8 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
         const int64_t m = m0 + mt * 16 + 4 * qd + i;
         if (m < M) {
           const float v = BITS == 4 ? acc[mt][t][i] : gacc[mt][t][i];
-          if (part == nullptr) y[m * ldy + n] = __builtin_fmaf(v, s8, bn);
-          else part[(z * M + m) * N + n] = v;
+          if (part == nullptr) y[m * ldy + n] = __builtin_fmaf(unscale(v, er[mt][i]), s8, bn);
+          else part[(z * M + m) * N + n] = v;      // still scaled by 2^rexp[m]
         }
       }
     }
@@ -805,8 +968,8 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
     const half8_t* __restrict__ planes, int64_t Mp, int64_t M,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
     int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n, int gm,
-    const float* __restrict__ bias, float* __restrict__ y, int64_t ldy, int64_t N,
-    float* __restrict__ part) {
+    const int* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y,
+    int64_t ldy, int64_t N, float* __restrict__ part) {
   constexpr int MTW = 4, NTW = 4, BM = 64;
   constexpr int PLANE = BM * 16;                        // entries per plane
   constexpr int RAWN = BITS == 4 ? 1 : 2;               // 64-byte windows per stage
@@ -947,6 +1110,11 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
       }
   }
 
+  int er[MTW][4];
+#pragma unroll
+  for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) er[mt][i] = rexp[m0 + mt * 16 + 4 * qd + i];
 #pragma unroll
   for (int t = 0; t < NTW; t++) {
     const int64_t n = n0 + t * 16 + c;
@@ -963,8 +1131,8 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
         const int64_t m = m0 + mt * 16 + 4 * qd + i;
         if (m < M) {
           const float v = acc[mt][t][i];
-          if (part == nullptr) y[m * ldy + n] = __builtin_fmaf(v, s8, bn);
-          else part[(z * M + m) * N + n] = v;
+          if (part == nullptr) y[m * ldy + n] = __builtin_fmaf(unscale(v, er[mt][i]), s8, bn);
+          else part[(z * M + m) * N + n] = v;      // still scaled by 2^rexp[m]
         }
       }
     }
@@ -1049,10 +1217,14 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const int2* __restri
 }
 
 // y[m, n] = (sum over z of part[z, m, n]) (* INT8 row scale) + bias, z in
-// order.  VEC: four consecutive n per thread (N % 4 == 0, y rows 16-byte aligned).
+// order.  Partial z of row m is scaled by 2^pexp[z * pz + m] (pz = 0: one
+// exponent per row for every slice); the slices meet in the domain of the
+// row's smallest exponent E and the sum is scaled back by 2^-E once.
+// VEC: four consecutive n per thread (N % 4 == 0, y rows 16-byte aligned).
 template <int BITS, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S,
                                                             int64_t M, int64_t N,
+                                                            const int* __restrict__ pexp, int64_t pz,
                                                             const uint16_t* __restrict__ sc,
                                                             const float* __restrict__ bias,
                                                             float* __restrict__ y, int64_t ldy) {
@@ -1061,12 +1233,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   for (int64_t o = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V; o < total;
        o += (int64_t)gridDim.x * blockDim.x * V) {
     const int64_t m = o / N, n = o - m * N;
+    int e = pexp[m];
+    for (int zz = 1; zz < S && pz != 0; zz++) e = min(e, pexp[zz * pz + m]);
     float v[V];
 #pragma unroll
     for (int u = 0; u < V; u++) v[u] = 0.0f;
     // Slices are added in order; the loads of up to 8 slices are issued
     // before their adds, so 8 slices cost one memory round trip.
-    auto add = [&](const float4& p) { v[0] += p.x; if constexpr (VEC) { v[1] += p.y; v[2] += p.z; v[3] += p.w; } };
+    auto add = [&](const float4& p, int zz) {
+      const int d = pz != 0 ? e - pexp[zz * pz + m] : 0;
+      v[0] += __builtin_amdgcn_ldexpf(p.x, d);
+      if constexpr (VEC) {
+        v[1] += __builtin_amdgcn_ldexpf(p.y, d);
+        v[2] += __builtin_amdgcn_ldexpf(p.z, d);
+        v[3] += __builtin_amdgcn_ldexpf(p.w, d);
+      }
+    };
     auto load = [&](int zz) {
       if constexpr (VEC) return *reinterpret_cast<const float4*>(part + zz * total + o);
       else return float4{part[zz * total + o], 0.0f, 0.0f, 0.0f};
@@ -1077,7 +1259,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 #pragma unroll
       for (int j = 0; j < 8; j++) p[j] = load(zz + j);
 #pragma unroll
-      for (int j = 0; j < 8; j++) add(p[j]);
+      for (int j = 0; j < 8; j++) add(p[j], zz + j);
     }
     if (zz < S) {
       float4 p[8];
@@ -1085,13 +1267,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
       for (int j = 0; j < 8; j++) p[j] = load(zz + j < S ? zz + j : zz);
 #pragma unroll
       for (int j = 0; j < 8; j++)
-        if (zz + j < S) add(p[j]);
+        if (zz + j < S) add(p[j], zz + j);
     }
 #pragma unroll
     for (int u = 0; u < V; u++) {
       float s8 = 1.0f;
       if constexpr (BITS == 8) s8 = f16_bits_to_f32(sc[n + u]);
-      v[u] = __builtin_fmaf(v[u], s8, bias ? bias[n + u] : 0.0f);
+      v[u] = __builtin_fmaf(unscale(v[u], e), s8, bias ? bias[n + u] : 0.0f);
     }
     if constexpr (VEC) *reinterpret_cast<float4*>(y + m * ldy + n) = float4{v[0], v[1], v[2], v[3]};
     else y[m * ldy + n] = v[0];
@@ -1186,7 +1368,15 @@ constexpr int64_t kGemmWsMinM = 33;         // warp-specialized DMA kernel from 
 constexpr int64_t kGemmWsMinM8 = 65;        // the same for INT8
 constexpr int64_t kGemmWsTargetBlocks = 256;  // one resident workgroup per CU (LDS ring)
 
+inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
 enum class Path { Skinny, Gemm, Generic };
+
+struct Plan;
+struct GemmWs {
+  size_t rexp_off = 0, part_off = 0, total = 0;
+};
+GemmWs gemm_ws_layout(const Plan& p);
 
 struct Plan {
   Path path;
@@ -1216,6 +1406,7 @@ struct Plan {
   int64_t ksplit = 1;   // skinny: K slices across workgroup rows (partials + reduction when > 1)
   int64_t split_units = 0;  // skinny: units per K slice
   size_t ws = 0;        // workspace bytes
+  int64_t m = 0, n = 0; // the linear's batch rows and out_features
 };
 
 // pairs: N rows interleave gate and up weights by 16-row tiles; a skinny
@@ -1224,6 +1415,8 @@ struct Plan {
 Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp, bool pairs = false,
                bool split = false) {
   Plan p;
+  p.m = m;
+  p.n = n;
   const bool tiled = bits == 4 ? (g == 128) : (k % 64 == 0);
   if (!tiled) { p.path = Path::Generic; return p; }
   p.nunits = bits == 4 ? kp / 128 : k / 64;
@@ -1341,8 +1534,10 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
                 (abytes <= kSkinnyLdsA && (kSkinnyLdsA / abytes) * kCUs >= groups);
     }
     if (!p.a_lds) p.pitch = p.nT;
-    p.ws = p.a_lds ? 0 : (size_t)(128 * p.pitch * m);
-    if (p.ksplit > 1) p.ws = (size_t)(4 * p.ksplit * m * n);   // partials (staging is in LDS)
+    // Pre-pass staging: the staged rows, then one scale exponent per row.
+    p.ws = p.a_lds ? 0 : align256((size_t)(128 * p.pitch * m)) + (size_t)(4 * m);
+    // K split: partials, then their exponents (staging is in LDS)
+    if (p.ksplit > 1) p.ws = align256((size_t)(4 * p.ksplit * m * n)) + (size_t)(4 * p.ksplit * m);
     return p;
   }
   const int64_t keff = p.nT * 32;
@@ -1378,10 +1573,18 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
     const int64_t per_mtile = 16 * p.mtw * keff * 4;
     p.gm = (int)std::max<int64_t>(1, std::min<int64_t>(p.tiles_m, (2 << 20) / per_mtile));
   }
-  // Operand planes (2 x 16 bytes per entry), then split-K partials.
-  p.ws = (size_t)(2 * 16 * p.nstages * p.mpad * 16) +
-         (p.splits > 1 ? (size_t)(4 * p.splits * m * n) : 0);
+  // Operand planes (2 x 16 bytes per entry), the row exponents, then
+  // split-K partials (gemm_ws_layout).
+  p.ws = gemm_ws_layout(p).total;
   return p;
+}
+
+GemmWs gemm_ws_layout(const Plan& p) {
+  GemmWs w;
+  w.rexp_off = align256((size_t)(2 * 16 * p.nstages * p.mpad * 16));
+  w.part_off = align256(w.rexp_off + (size_t)(4 * p.mpad));
+  w.total = p.splits > 1 ? w.part_off + (size_t)(4 * p.splits * p.m * p.n) : w.rexp_off + (size_t)(4 * p.mpad);
+  return w;
 }
 
 inline bool x_vectorizable(const float* x, int64_t ldx, int64_t k) {
@@ -1392,13 +1595,13 @@ template <int BITS, bool LDS, bool HL, bool SVEC, bool M1, bool REM>
 void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStream_t st,
                       const float* x, int64_t ldx, int64_t m, int64_t k, bool xvec,
                       const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
-                      const half8_t* xa, const float* bias, float* y, int64_t ldy, int64_t n,
-                      int2* argp) {
+                      const half8_t* xa, const int* xexp, const float* bias, float* y,
+                      int64_t ldy, int64_t n, int2* argp, int* pexp) {
   const int pairs = p.pairs ? 1 : 0;
 #define KQ_SKINNY(KS_, NT_)                                                                   \
   skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC, M1, REM><<<grid, block, shm, st>>>(            \
       x, ldx, (int)m, k, xvec, wq, sc, row_bytes, ng, p.nunits, p.per_wave, (int)p.pitch, xa, \
-      bias, y, ldy, n, argp, pairs, p.split_units, m * n)
+      xexp, bias, y, ldy, n, argp, pairs, p.split_units, m * n, pexp)
   if (p.nt == 4) {
     if (p.ks == 2) KQ_SKINNY(2, 4); else KQ_SKINNY(4, 4);
   } else if (p.nt == 2) {
@@ -1425,29 +1628,33 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
                   int2* argp = nullptr) {
   const bool xvec = x_vectorizable(x, ldx, k);
   const half8_t* xa = nullptr;
+  const int* xexp = nullptr;
   if (!p.a_lds) {
+    // Staged by a pre-pass, one workgroup per row (row scale over all of K).
     half8_t* a = static_cast<half8_t*>(ws);
-    const int64_t entries = p.nT * 4 * m;
-    const unsigned sg = (unsigned)std::min<int64_t>((entries + 255) / 256, 4096);
+    int* e = reinterpret_cast<int*>(static_cast<char*>(ws) + align256((size_t)(128 * p.pitch * m)));
     if (p.hl)
-      stage_skinny_kernel<BITS, true><<<sg, 256, 0, st>>>(x, ldx, (int)m, k, (int)p.nT, p.pitch, xvec, a);
+      stage_rows_kernel<BITS, false, true><<<(unsigned)m, 256, 0, st>>>(x, ldx, (int)m, k, (int)p.nT, p.pitch, 0, xvec, a, e);
     else
-      stage_skinny_kernel<BITS, false><<<sg, 256, 0, st>>>(x, ldx, (int)m, k, (int)p.nT, p.pitch, xvec, a);
+      stage_rows_kernel<BITS, false, false><<<(unsigned)m, 256, 0, st>>>(x, ldx, (int)m, k, (int)p.nT, p.pitch, 0, xvec, a, e);
     xa = a;
+    xexp = e;
   }
   const size_t red = (size_t)p.waves * p.nt * 256 * sizeof(float);
   const size_t abytes = p.a_lds ? (size_t)(128 * p.pitch * m) : 0;
-  const size_t shm = std::max(red, abytes);
+  const size_t shm = std::max(red, abytes) + (size_t)p.waves * 16 * sizeof(int);  // + row exponents
   const dim3 grid((unsigned)((n + 16 * p.nt - 1) / (16 * p.nt)), (unsigned)p.ksplit);
   // K split: the slices write partials (row scale applied, no bias) to the
   // workspace, [slice][m][n]; the reduction adds them in slice order + bias.
   float* const y_out = y;
   const int64_t ldy_out = ldy;
   const float* const bias_out = bias;
+  int* pexp = nullptr;
   if (p.ksplit > 1) {
     y = static_cast<float*>(ws);
     ldy = n;
     bias = nullptr;
+    pexp = reinterpret_cast<int*>(static_cast<char*>(ws) + align256((size_t)(4 * p.ksplit * m * n)));
   }
   const dim3 block((unsigned)(64 * p.waves));
   const bool svec = p.svec && reinterpret_cast<uintptr_t>(sc) % (2 * p.ks) == 0;
@@ -1455,12 +1662,12 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   do {                                                                                          \
     if (svec)                                                                                   \
       launch_skinny_ks<BITS, LDS_, HL_, true, M1_, REM_>(p, grid, block, shm, st, x, ldx, m, k, \
-                                                         xvec, wq, sc, row_bytes, ng, xa, bias, \
-                                                         y, ldy, n, argp);                      \
+                                                         xvec, wq, sc, row_bytes, ng, xa, xexp, \
+                                                         bias, y, ldy, n, argp, pexp);          \
     else                                                                                        \
       launch_skinny_ks<BITS, LDS_, HL_, false, M1_, REM_>(p, grid, block, shm, st, x, ldx, m,   \
                                                           k, xvec, wq, sc, row_bytes, ng, xa,   \
-                                                          bias, y, ldy, n, argp);               \
+                                                          xexp, bias, y, ldy, n, argp, pexp);   \
   } while (0)
   // Do the pre-loads (one batch of KS units at M = 1, else 4 entries per
   // lane over all rows) cover every activation entry of every wave?  The
@@ -1474,7 +1681,8 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   // multiple of 128 leaves tail entries that must be staged as zeros).
   const bool aligned = xvec && k == p.nunits * kUnitCols;
   const bool one_row = BITS == 4 && aligned && m == 1 && p.per_wave * kTpu <= 16 * pre1;
-  const bool covered = aligned && m * p.per_wave * kTpu <= 16 * 4;
+  // (lane mapping: skinny_lanes_per_row(m) lanes per row, 4 pre-load slots each)
+  const bool covered = aligned && p.per_wave * kTpu <= skinny_lanes_per_row((int)m);
   if (p.a_lds) {
     if constexpr (BITS == 4) {
       if (p.hl && one_row) {
@@ -1496,20 +1704,20 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
     const int64_t items = vec ? m * n / 4 : m * n;
     const unsigned rg = (unsigned)std::min<int64_t>((items + 255) / 256, 8192);
     // BITS = 4 instance: sums only (the slices applied any INT8 row scale)
-    if (vec) splitk_reduce_kernel<4, true><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, nullptr, bias_out, y_out, ldy_out);
-    else splitk_reduce_kernel<4, false><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, nullptr, bias_out, y_out, ldy_out);
+    if (vec) splitk_reduce_kernel<4, true><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, pexp, m, nullptr, bias_out, y_out, ldy_out);
+    else splitk_reduce_kernel<4, false><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, pexp, m, nullptr, bias_out, y_out, ldy_out);
   }
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }
 
 template <int BITS, int MTW, int NTW, int WN = kGemmWN>
-void launch_gemm_t(const Plan& p, const half8_t* planes, int64_t m, const uint8_t* wq,
-                   const uint16_t* sc, int64_t row_bytes, int64_t ng, const float* bias, float* y,
-                   int64_t ldy, int64_t n, float* part, hipStream_t st) {
+void launch_gemm_t(const Plan& p, const half8_t* planes, const int* rexp, int64_t m,
+                   const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
+                   const float* bias, float* y, int64_t ldy, int64_t n, float* part, hipStream_t st) {
   const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
   gemm_kernel<BITS, MTW, NTW, WN><<<blocks, 64 * WN, 0, st>>>(
       planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m, (int)p.tiles_n,
-      p.gm, bias, y, ldy, n, part);
+      p.gm, rexp, bias, y, ldy, n, part);
 }
 
 template <int BITS>
@@ -1517,17 +1725,18 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
                 const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                 const float* bias, float* y, int64_t ldy, int64_t n, void* ws, hipStream_t st) {
   half8_t* planes = static_cast<half8_t*>(ws);
-  const int64_t entries = p.nstages * p.mpad * 16;
-  const unsigned sg = (unsigned)std::min<int64_t>((entries + 255) / 256, 8192);
-  stage_planes_kernel<BITS><<<sg, 256, 0, st>>>(x, ldx, m, k, p.nstages, p.mpad,
-                                                x_vectorizable(x, ldx, k), planes);
-  float* part = p.splits > 1 ? reinterpret_cast<float*>(planes + 2 * entries) : nullptr;
+  const GemmWs lay = gemm_ws_layout(p);
+  int* rexp = reinterpret_cast<int*>(static_cast<char*>(ws) + lay.rexp_off);
+  // One workgroup per (padded) row: the row's scale, then its operand planes.
+  stage_rows_kernel<BITS, true, false><<<(unsigned)p.mpad, 256, 0, st>>>(
+      x, ldx, (int)m, k, (int)(4 * p.nstages), 0, p.mpad, x_vectorizable(x, ldx, k), planes, rexp);
+  float* part = p.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + lay.part_off) : nullptr;
   if (p.wspec) {
     const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
 #define KQ_WS(D_, NC_)                                                                          \
   gemm_ws_kernel<BITS, D_, NC_><<<blocks, 64 * (NC_ + 1), 0, st>>>(                            \
       planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m,               \
-      (int)p.tiles_n, p.gm, bias, y, ldy, n, part)
+      (int)p.tiles_n, p.gm, rexp, bias, y, ldy, n, part)
     if constexpr (BITS == 4) {
       if (p.wsnc == kWsWideNC) KQ_WS(2, kWsWideNC);
       else KQ_WS(3, kWsNC);
@@ -1536,20 +1745,20 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
     }
 #undef KQ_WS
   } else if (p.mtw == 2) {
-    if (p.ntw == 2) launch_gemm_t<BITS, 2, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
-    else if (p.wn == kGemmWideWN8) launch_gemm_t<BITS, 2, 4, kGemmWideWN8>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
-    else launch_gemm_t<BITS, 2, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    if (p.ntw == 2) launch_gemm_t<BITS, 2, 2>(p, planes, rexp, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    else if (p.wn == kGemmWideWN8) launch_gemm_t<BITS, 2, 4, kGemmWideWN8>(p, planes, rexp, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    else launch_gemm_t<BITS, 2, 4>(p, planes, rexp, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   } else {
-    if (p.ntw == 2) launch_gemm_t<BITS, 4, 2>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
-    else launch_gemm_t<BITS, 4, 4>(p, planes, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    if (p.ntw == 2) launch_gemm_t<BITS, 4, 2>(p, planes, rexp, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
+    else launch_gemm_t<BITS, 4, 4>(p, planes, rexp, m, wq, sc, row_bytes, ng, bias, y, ldy, n, part, st);
   }
   if (part) {
     const bool vec = n % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
                      (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
     const int64_t items = vec ? m * n / 4 : m * n;
     const unsigned rg = (unsigned)std::min<int64_t>((items + 255) / 256, 8192);
-    if (vec) splitk_reduce_kernel<BITS, true><<<rg, 256, 0, st>>>(part, (int)p.splits, m, n, sc, bias, y, ldy);
-    else splitk_reduce_kernel<BITS, false><<<rg, 256, 0, st>>>(part, (int)p.splits, m, n, sc, bias, y, ldy);
+    if (vec) splitk_reduce_kernel<BITS, true><<<rg, 256, 0, st>>>(part, (int)p.splits, m, n, rexp, 0, sc, bias, y, ldy);
+    else splitk_reduce_kernel<BITS, false><<<rg, 256, 0, st>>>(part, (int)p.splits, m, n, rexp, 0, sc, bias, y, ldy);
   }
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (gemm)" : "kq_linear_int8 (gemm)");
 }
@@ -1571,7 +1780,6 @@ struct ArgLayout {
   size_t part_off = 0, logit_off = 0, total = 0;
 };
 
-inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 ArgLayout arg_layout(const Plan& p, int64_t m, int64_t n) {
   ArgLayout a;

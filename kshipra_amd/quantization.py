@@ -220,7 +220,7 @@ def _dequantize_int8_per_channel(qw: QuantizedWeight,
     n, k = qw.original_shape
     od = _out_dtype(dtype)
     out = torch.empty((n, k), dtype=od, device=qw.payload.device)
-    p, s = qw.payload.contiguous(), qw.scales.contiguous()
+    p, s = qw.payload.contiguous(), _fp16_scales(qw.scales)
     _lib.check(lib.kq_dequantize_int8(p.data_ptr(), s.data_ptr(), n, k, out.data_ptr(),
                                       _lib.DTYPE_CODE[od], _lib.stream_of(p)))
     return out if od == dtype else out.to(dtype)
@@ -268,7 +268,7 @@ def _dequantize_int4_per_group(qw: QuantizedWeight,
     n, k = qw.original_shape
     od = _out_dtype(dtype)
     out = torch.empty((n, k), dtype=od, device=qw.payload.device)
-    p, s = qw.payload.contiguous(), qw.scales.contiguous()
+    p, s = qw.payload.contiguous(), _fp16_scales(qw.scales)
     _lib.check(lib.kq_dequantize_int4(p.data_ptr(), s.data_ptr(), n, k, qw.group_size,
                                       qw.in_features_padded, out.data_ptr(),
                                       _lib.DTYPE_CODE[od], _lib.stream_of(p)))
@@ -280,51 +280,97 @@ def _dequantize_int4_per_group(qw: QuantizedWeight,
 # ---------------------------------------------------------------------- #
 
 
-def quantized_linear(x: torch.Tensor, qw: QuantizedWeight,
-                     bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``F.linear(x, qw.dequantize(x.dtype), bias)`` without materialising the
-    weight: one fused HIP dequant-matmul over the packed payload."""
+class _Operands:
+    """Device operands of one dequant-matmul call, checked before any launch."""
+
+    __slots__ = ("x2", "ldx", "m", "payload", "scales", "bias", "stream", "lib")
+
+
+def _fp16_scales(scales: torch.Tensor) -> torch.Tensor:
+    """The kernels read fp16 scales (what the quantizers store).  Scales of
+    another float dtype are accepted when fp16 holds them exactly -- the
+    reference's ``scales.to(torch.float32)`` (engine/quantization.py:228, :339)
+    then sees the same values -- and refused otherwise."""
+    if scales.dtype == torch.float16:
+        return scales.contiguous()
+    if not scales.dtype.is_floating_point:
+        raise QuantizationError(f"scales must be a float tensor, got {scales.dtype}")
+    s16 = scales.to(torch.float16)
+    if not torch.equal(s16.to(scales.dtype), scales):
+        raise QuantizationError(
+            f"scales of dtype {scales.dtype} are not exactly representable in float16")
+    return s16.contiguous()
+
+
+def _operands(x: torch.Tensor, qw: QuantizedWeight, bias: Optional[torch.Tensor],
+              out_features: int) -> _Operands:
+    """Shape, device and dtype checks shared by every dequant-matmul entry.
+
+    As ``F.linear`` would: a mismatched inner dimension and operands on
+    different devices raise ``RuntimeError`` (the reference's payload is a
+    plain attribute that ``module.to()`` leaves behind, engine/quantization.py:
+    383-392, while its bias buffer moves).  The payload and fp16 scales are
+    made contiguous, the bias fp32 and contiguous; ``x`` is viewed as a
+    ``[M, in_features]`` fp32 matrix with unit column stride.
+    """
     _lib.require_device(x, "input")
-    out_features, in_features = qw.original_shape
+    in_features = qw.original_shape[1]
     if x.shape[-1] != in_features:
         raise RuntimeError(
             f"mat1 and mat2 shapes cannot be multiplied "
             f"({x.numel() // max(x.shape[-1], 1)}x{x.shape[-1]} and {in_features}x{out_features})")
-    if x.device != qw.payload.device:
-        raise RuntimeError(f"input on {x.device} but weight on {qw.payload.device}")
-    lib = _lib.load()
-    out_dtype = x.dtype
+    for name, t in (("weight payload", qw.payload), ("weight scales", qw.scales),
+                    ("bias", bias)):
+        if t is not None and t.device != x.device:
+            raise RuntimeError(f"input on {x.device} but {name} on {t.device}")
+    if bias is not None and tuple(bias.shape) != (out_features,):
+        raise RuntimeError(f"bias shape {tuple(bias.shape)} != ({out_features},)")
+    op = _Operands()
+    op.lib = _lib.load()
     x2 = x.reshape(-1, in_features)
     if x2.dtype != torch.float32:
         x2 = x2.to(torch.float32)
     if x2.stride(1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < in_features):
         x2 = x2.contiguous()
-    m = x2.shape[0]
+    op.x2, op.m = x2, x2.shape[0]
+    op.ldx = x2.stride(0) if op.m > 1 else in_features
+    op.payload = qw.payload.contiguous()
+    op.scales = _fp16_scales(qw.scales)
+    op.bias = None
+    if bias is not None:
+        b = bias.detach()
+        if b.dtype != torch.float32 or not b.is_contiguous():
+            b = b.to(torch.float32).contiguous()
+        op.bias = b
+    op.stream = _lib.stream_of(x2)
+    return op
+
+
+def quantized_linear(x: torch.Tensor, qw: QuantizedWeight,
+                     bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``F.linear(x, qw.dequantize(x.dtype), bias)`` without materialising the
+    weight: one fused HIP dequant-matmul over the packed payload."""
+    out_features, in_features = qw.original_shape
+    op = _operands(x, qw, bias, out_features)
+    lib, m = op.lib, op.m
     y = torch.empty((m, out_features), dtype=torch.float32, device=x.device)
     if m > 0:
-        b = None
-        if bias is not None:
-            b = bias.detach()
-            if b.dtype != torch.float32 or not b.is_contiguous():
-                b = b.to(torch.float32).contiguous()
-        ldx = x2.stride(0) if m > 1 else in_features
-        stream = _lib.stream_of(x2)
+        args = (op.x2.data_ptr(), m, op.ldx, op.payload.data_ptr(), op.scales.data_ptr())
         if qw.scheme == "int8_per_channel":
             nbytes = lib.kq_linear_workspace_bytes(8, m, out_features, in_features, 0)
-            ws = _lib.workspace(x.device, stream, nbytes)
+            ws = _lib.workspace(x.device, op.stream, nbytes)
             _lib.check(lib.kq_linear_int8(
-                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), _lib.ptr(b),
-                y.data_ptr(), out_features, out_features, in_features, _lib.ptr(ws), nbytes, stream))
+                *args, _lib.ptr(op.bias), y.data_ptr(), out_features, out_features, in_features,
+                _lib.ptr(ws), nbytes, op.stream))
         else:
             g = qw.group_size
             nbytes = lib.kq_linear_workspace_bytes(4, m, out_features, in_features, g)
-            ws = _lib.workspace(x.device, stream, nbytes)
+            ws = _lib.workspace(x.device, op.stream, nbytes)
             _lib.check(lib.kq_linear_int4(
-                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), g,
-                qw.in_features_padded, _lib.ptr(b), y.data_ptr(), out_features, out_features,
-                in_features, _lib.ptr(ws), nbytes, stream))
+                *args, g, qw.in_features_padded, _lib.ptr(op.bias), y.data_ptr(), out_features,
+                out_features, in_features, _lib.ptr(ws), nbytes, op.stream))
     y = y.reshape(*x.shape[:-1], out_features)
-    return y if out_dtype == torch.float32 else y.to(out_dtype)
+    return y if x.dtype == torch.float32 else y.to(x.dtype)
 
 
 def quantized_linear_argmax(x: torch.Tensor, qw: QuantizedWeight,
@@ -336,48 +382,28 @@ def quantized_linear_argmax(x: torch.Tensor, qw: QuantizedWeight,
     argmax in its epilogue; the logits are written only when
     ``return_logits`` is set.  Returns int64 tokens of shape ``x.shape[:-1]``
     (and the fp32 logits)."""
-    _lib.require_device(x, "input")
     out_features, in_features = qw.original_shape
-    if x.shape[-1] != in_features:
-        raise RuntimeError(
-            f"mat1 and mat2 shapes cannot be multiplied "
-            f"({x.numel() // max(x.shape[-1], 1)}x{x.shape[-1]} and {in_features}x{out_features})")
-    if x.device != qw.payload.device:
-        raise RuntimeError(f"input on {x.device} but weight on {qw.payload.device}")
-    lib = _lib.load()
-    x2 = x.reshape(-1, in_features)
-    if x2.dtype != torch.float32:
-        x2 = x2.to(torch.float32)
-    if x2.stride(1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < in_features):
-        x2 = x2.contiguous()
-    m = x2.shape[0]
+    op = _operands(x, qw, bias, out_features)
+    lib, m = op.lib, op.m
     tokens = torch.empty((m,), dtype=torch.int64, device=x.device)
     logits = (torch.empty((m, out_features), dtype=torch.float32, device=x.device)
               if return_logits else None)
     if m > 0:
-        b = None
-        if bias is not None:
-            b = bias.detach()
-            if b.dtype != torch.float32 or not b.is_contiguous():
-                b = b.to(torch.float32).contiguous()
-        ldx = x2.stride(0) if m > 1 else in_features
-        stream = _lib.stream_of(x2)
+        args = (op.x2.data_ptr(), m, op.ldx, op.payload.data_ptr(), op.scales.data_ptr())
         lp = _lib.ptr(logits)
         if qw.scheme == "int8_per_channel":
             nbytes = lib.kq_linear_argmax_workspace_bytes(8, m, out_features, in_features, 0)
-            ws = _lib.workspace(x.device, stream, nbytes)
+            ws = _lib.workspace(x.device, op.stream, nbytes)
             _lib.check(lib.kq_linear_argmax_int8(
-                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), _lib.ptr(b),
-                lp, out_features, out_features, in_features, tokens.data_ptr(), _lib.ptr(ws),
-                nbytes, stream))
+                *args, _lib.ptr(op.bias), lp, out_features, out_features, in_features,
+                tokens.data_ptr(), _lib.ptr(ws), nbytes, op.stream))
         else:
             g = qw.group_size
             nbytes = lib.kq_linear_argmax_workspace_bytes(4, m, out_features, in_features, g)
-            ws = _lib.workspace(x.device, stream, nbytes)
+            ws = _lib.workspace(x.device, op.stream, nbytes)
             _lib.check(lib.kq_linear_argmax_int4(
-                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), g,
-                qw.in_features_padded, _lib.ptr(b), lp, out_features, out_features, in_features,
-                tokens.data_ptr(), _lib.ptr(ws), nbytes, stream))
+                *args, g, qw.in_features_padded, _lib.ptr(op.bias), lp, out_features, out_features,
+                in_features, tokens.data_ptr(), _lib.ptr(ws), nbytes, op.stream))
     tokens = tokens.reshape(x.shape[:-1])
     if return_logits:
         return tokens, logits.reshape(*x.shape[:-1], out_features)
@@ -556,48 +582,28 @@ def quantized_gate_up_silu(x: torch.Tensor, qw: QuantizedWeight,
     interleaved weight of ``interleave_gate_up`` (and bias interleaved the
     same way), in one dequant-matmul launch whose epilogue applies the gate
     (M <= 16), or the matmul plus one pairing kernel."""
-    _lib.require_device(x, "input")
     rows, in_features = qw.original_shape
     nh = rows // 2
-    if x.shape[-1] != in_features:
-        raise RuntimeError(
-            f"mat1 and mat2 shapes cannot be multiplied "
-            f"({x.numel() // max(x.shape[-1], 1)}x{x.shape[-1]} and {in_features}x{rows})")
-    if x.device != qw.payload.device:
-        raise RuntimeError(f"input on {x.device} but weight on {qw.payload.device}")
-    lib = _lib.load()
-    out_dtype = x.dtype
-    x2 = x.reshape(-1, in_features)
-    if x2.dtype != torch.float32:
-        x2 = x2.to(torch.float32)
-    if x2.stride(1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < in_features):
-        x2 = x2.contiguous()
-    m = x2.shape[0]
+    op = _operands(x, qw, bias, rows)
+    lib, m = op.lib, op.m
     act = torch.empty((m, nh), dtype=torch.float32, device=x.device)
     if m > 0:
-        b = None
-        if bias is not None:
-            b = bias.detach()
-            if b.dtype != torch.float32 or not b.is_contiguous():
-                b = b.to(torch.float32).contiguous()
-        ldx = x2.stride(0) if m > 1 else in_features
-        stream = _lib.stream_of(x2)
+        args = (op.x2.data_ptr(), m, op.ldx, op.payload.data_ptr(), op.scales.data_ptr())
         if qw.scheme == "int8_per_channel":
             nbytes = lib.kq_linear_silu_mul_workspace_bytes(8, m, nh, in_features, 0)
-            ws = _lib.workspace(x.device, stream, nbytes)
+            ws = _lib.workspace(x.device, op.stream, nbytes)
             _lib.check(lib.kq_linear_silu_mul_int8(
-                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), _lib.ptr(b),
-                act.data_ptr(), nh, nh, in_features, _lib.ptr(ws), nbytes, stream))
+                *args, _lib.ptr(op.bias), act.data_ptr(), nh, nh, in_features, _lib.ptr(ws),
+                nbytes, op.stream))
         else:
             g = qw.group_size
             nbytes = lib.kq_linear_silu_mul_workspace_bytes(4, m, nh, in_features, g)
-            ws = _lib.workspace(x.device, stream, nbytes)
+            ws = _lib.workspace(x.device, op.stream, nbytes)
             _lib.check(lib.kq_linear_silu_mul_int4(
-                x2.data_ptr(), m, ldx, qw.payload.data_ptr(), qw.scales.data_ptr(), g,
-                qw.in_features_padded, _lib.ptr(b), act.data_ptr(), nh, nh, in_features,
-                _lib.ptr(ws), nbytes, stream))
+                *args, g, qw.in_features_padded, _lib.ptr(op.bias), act.data_ptr(), nh, nh,
+                in_features, _lib.ptr(ws), nbytes, op.stream))
     act = act.reshape(*x.shape[:-1], nh)
-    return act if out_dtype == torch.float32 else act.to(out_dtype)
+    return act if x.dtype == torch.float32 else act.to(x.dtype)
 
 
 class FusedGateUpSiLU(nn.Module):

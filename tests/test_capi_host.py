@@ -49,19 +49,21 @@ def test_workspace_query_is_host_only():
     assert lib.kq_linear_workspace_bytes(8, 1, 4096, 14336, 0) == 0
     # M = 8, K = 4096: 132 KiB of staged activations per workgroup; 256
     # workgroups (one per CU) stage in LDS, 448 (a second round) in the
-    # workspace, 4 bytes per activation
+    # workspace, 4 bytes per activation, then one scale exponent per row
     assert lib.kq_linear_workspace_bytes(8, 8, 4096, 4096, 0) == 0
-    assert lib.kq_linear_workspace_bytes(8, 8, 28672, 4096, 0) == 4 * 8 * 4096
+    assert lib.kq_linear_workspace_bytes(8, 8, 28672, 4096, 0) == 4 * 8 * 4096 + 4 * 8
     # K = 14336, M >= 3: K split into slices staged in LDS; the workspace
-    # holds one fp32 partial output per slice (8 slices at M = 8, 4 at M = 4 and 3)
-    assert lib.kq_linear_workspace_bytes(4, 8, 4096, 14336, 128) == 8 * 4 * 8 * 4096
-    assert lib.kq_linear_workspace_bytes(8, 4, 4096, 14336, 0) == 4 * 4 * 4 * 4096
-    assert lib.kq_linear_workspace_bytes(8, 3, 4096, 14336, 0) == 4 * 4 * 3 * 4096
+    # holds one fp32 partial output per slice (8 slices at M = 8, 4 at M = 4
+    # and 3), then one scale exponent per (slice, row)
+    assert lib.kq_linear_workspace_bytes(4, 8, 4096, 14336, 128) == 8 * 4 * 8 * 4096 + 4 * 8 * 8
+    assert lib.kq_linear_workspace_bytes(8, 4, 4096, 14336, 0) == 4 * 4 * 4 * 4096 + 4 * 4 * 4
+    assert lib.kq_linear_workspace_bytes(8, 3, 4096, 14336, 0) == 4 * 4 * 3 * 4096 + 4 * 4 * 3
     # ... below M = 3, whole-K workgroups stage x in LDS: no workspace
     assert lib.kq_linear_workspace_bytes(4, 2, 4096, 14336, 128) == 0
-    # GEMM path: M rounded up to the 64-row tile
-    assert lib.kq_linear_workspace_bytes(4, 512, 14336, 4096, 128) == 4 * 512 * 4096
-    assert lib.kq_linear_workspace_bytes(4, 100, 64, 256, 128) == 4 * 128 * 256
+    # GEMM path: operand planes for M rounded up to the 64-row tile, then one
+    # scale exponent per padded row
+    assert lib.kq_linear_workspace_bytes(4, 512, 14336, 4096, 128) == 4 * 512 * 4096 + 4 * 512
+    assert lib.kq_linear_workspace_bytes(4, 100, 64, 256, 128) == 4 * 128 * 256 + 4 * 128
     # generic path (G != 128) needs none
     assert lib.kq_linear_workspace_bytes(4, 64, 512, 512, 32) == 0
     assert lib.kq_linear_workspace_bytes(4, 0, 10, 10, 128) == 0
@@ -287,3 +289,52 @@ def test_silu_mul_workspace_and_argument_errors():
     assert lib.kq_linear_silu_mul_int4(1, 1, 128, 1, 1, 128, 128, None, None, 32, 32, 128, None, 0,
                                        None) == _lib.KQ_ERR_ARG
     assert lib.kq_last_error() not in (None, b"")
+
+
+def test_graph_workspaces_are_retained(monkeypatch):
+    """Calls under HIP graph capture get workspaces that no eager call or
+    other capture shares and that are never released while a graph may
+    replay: a buffer superseded inside a capture is retired, not freed."""
+    import weakref
+
+    cid = {"v": None}
+    monkeypatch.setattr(_lib, "_capture_id", lambda stream: cid["v"])
+    monkeypatch.setattr(_lib, "_alloc", lambda dev, n: torch.empty(n, dtype=torch.uint8))
+    monkeypatch.setattr(_lib, "_ws", {})
+    monkeypatch.setattr(_lib, "_graph_ws", {})
+    monkeypatch.setattr(_lib, "_graph_retired", [])
+    dev = torch.device("cuda", 0)
+    eager = _lib.workspace(dev, 7, 100)
+    assert _lib.workspace(dev, 7, 100) is eager                 # eager calls share per stream
+    cid["v"] = 11                                               # capture 11 on stream 7
+    g1 = _lib.workspace(dev, 7, 100)
+    assert g1 is not eager and _lib.workspace(dev, 7, 50) is g1  # shared within the capture
+    g1_ref = weakref.ref(g1)
+    g1_big = _lib.workspace(dev, 7, 4 << 20)                    # grows inside the capture
+    assert g1_big is not g1
+    del g1
+    assert g1_ref() is not None                                 # the superseded buffer stays alive
+    cid["v"] = 12                                               # another capture
+    g2 = _lib.workspace(dev, 7, 100)
+    assert g2 is not g1_big and g2 is not eager
+    cid["v"] = None                                             # eager again, larger
+    eager_big = _lib.workspace(dev, 7, 8 << 20)
+    assert eager_big is not eager and eager_big is not g1_big and eager_big is not g2
+    assert _lib.workspace(dev, 7, 0) is None
+    _lib.release_graph_workspaces()
+    assert g1_ref() is None                                     # released on request only
+
+
+def test_scales_conversion_rules():
+    """fp16 scales pass through; other float scales only when fp16 holds them
+    exactly (the reference reads them with .to(float32)); others refuse."""
+    from kshipra_amd.quantization import QuantizationError, _fp16_scales
+    s16 = torch.tensor([0.5, 2.0 ** -20, 65504.0], dtype=torch.float16)
+    assert _fp16_scales(s16) is s16 or torch.equal(_fp16_scales(s16), s16)
+    assert torch.equal(_fp16_scales(s16.float()), s16)
+    sb = torch.tensor([0.5, 2.0 ** -20, 3.0], dtype=torch.bfloat16)
+    assert torch.equal(_fp16_scales(sb), sb.half())
+    with pytest.raises(QuantizationError):
+        _fp16_scales(torch.tensor([0.1], dtype=torch.float32))
+    with pytest.raises(QuantizationError):
+        _fp16_scales(torch.tensor([1], dtype=torch.int32))

@@ -77,6 +77,34 @@ def test_loader_validates(tmp_path):
     torch.save(d, str(tmp_path / "bad.pt"))
     with pytest.raises(QuantizationError):                # scales shape disagrees with the payload
         load_quantized(str(tmp_path / "bad.pt"))
-    torch.save({"payload": qw.payload, "scales": qw.scales}, str(tmp_path / "bare.pt"))
-    with pytest.raises(QuantizationError, match="lacks"):  # the bare reference dict has no metadata
-        load_quantized(str(tmp_path / "bare.pt"))
+    d.pop("scheme")
+    torch.save(d, str(tmp_path / "partial.pt"))
+    with pytest.raises(QuantizationError, match="lacks"):  # metadata present but incomplete
+        load_quantized(str(tmp_path / "partial.pt"))
+
+
+@pytest.mark.parametrize("scheme,k", [("int8", 300), ("int4", 256), ("int4", 300)])
+def test_reference_bare_dict(tmp_path, scheme, k):
+    """The reference's own file (tests/test_quantization.py:312 saves
+    ``{"payload", "scales"}`` and nothing else): scheme, shape and group size
+    are inferred; a padded INT4 K comes from the caller."""
+    qw = _oracle_qw(gaussian((24, k), seed=k), scheme)
+    path = str(tmp_path / "bare.pt")
+    torch.save({"payload": qw.payload, "scales": qw.scales}, path)
+    padded = scheme == "int4" and k % 128 != 0
+    _same(load_quantized(path, in_features=k if padded else None), qw)
+    if padded:
+        got = load_quantized(path)                           # K read as the padded width
+        assert got.original_shape == (24, qw.in_features_padded)
+        assert torch.equal(got.payload, qw.payload)
+        with pytest.raises(QuantizationError):
+            load_quantized(path, in_features=k - 128)        # outside the last group
+    if scheme == "int4":
+        with pytest.raises(QuantizationError):
+            load_quantized(path, in_features=k if padded else None, group_size=64)
+    else:
+        with pytest.raises(QuantizationError):
+            load_quantized(path, in_features=k + 1)
+    torch.save({"payload": qw.payload.to(torch.int16), "scales": qw.scales}, path)
+    with pytest.raises(QuantizationError):
+        load_quantized(path)

@@ -66,3 +66,39 @@ def test_decoder_from_saved_quantized_weights(gpu, tmp_path, scheme):
     lm2 = DecoderLM(DecoderConfig(**cfg), extra, scheme, gpu, max_seq=32, quantized=loaded, fuse=True)
     toks2, _ = lm2.generate([3, 14, 15, 92], 6)
     assert toks2 == toks
+
+
+@pytest.mark.parametrize("scheme,n,k", [("int8", 1024, 896), ("int4", 1024, 896), ("int4", 640, 1000)])
+@pytest.mark.parametrize("m", [1, 8, 40])
+def test_oracle_bytes_from_disk_match_float64(gpu, tmp_path, scheme, n, k, m):
+    """The oracle's quantized bytes saved as the reference's bare
+    ``{"payload", "scales"}`` dict (tests/test_quantization.py:312), loaded
+    straight into HBM and multiplied by the HIP kernel: the output equals the
+    float64 product of the oracle's exact dequantized weight within the
+    linear path's bars (1e-4 norm-wise and element-wise)."""
+    import numpy as np
+    from cases import gaussian
+    from oracle import quant
+
+    w = gaussian((n, k), seed=n + k + m)
+    b = gaussian((n,), seed=n + 1)
+    if scheme == "int8":
+        p, s = quant.c_quantize_int8(w)
+        w_hat = quant.c_dequantize_int8(p, s)
+    else:
+        p, s, _ = quant.c_quantize_int4(w, 128)
+        w_hat = quant.c_dequantize_int4(p, s, k, 128)
+    path = str(tmp_path / "w.pt")
+    torch.save({"payload": torch.from_numpy(p), "scales": torch.from_numpy(s)}, path)
+    qw = load_quantized(path, gpu, in_features=k)
+    assert qw.payload.device == gpu and qw.scales.device == gpu
+    assert np.array_equal(qw.payload.cpu().numpy(), p)
+    x = gaussian((m, k), seed=m, std=1.0)
+    y = quantized_linear(torch.from_numpy(x).to(gpu), qw, torch.from_numpy(b).to(gpu))
+    y = y.cpu().numpy().astype(np.float64)
+    y64 = quant.linear_f64(x, w_hat, b)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(w_hat.astype(np.float64)).T + np.abs(b)
+    err = np.abs(y - y64)
+    norm, elem = err.max() / np.abs(y64).max(), (err / mag).max()
+    print(f"[disk {scheme} m={m} n={n} k={k}] norm-wise {norm:.3e} element-wise {elem:.3e}", flush=True)
+    assert norm <= 1e-4 and elem <= 1e-4

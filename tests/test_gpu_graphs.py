@@ -86,3 +86,36 @@ def test_graph_replays_match_eager(gpu):
             for name, ref in eager.items():
                 assert torch.equal(outs[name], ref), (rep, name)
             assert torch.equal(pool, pool_eager), rep
+
+
+def test_captured_workspace_survives_eager_growth(gpu):
+    """A graph keeps the workspace address its launches were recorded with.
+    After capture, an eager call on the same stream that needs a larger
+    workspace and a fresh allocation filled with a pattern must neither
+    change the replayed result nor be overwritten by the replay."""
+    w = torch.from_numpy(gaussian((4096, 14336), seed=3)).to(gpu)
+    q = quantize_int8_per_channel(w)                     # M = 8: K-split skinny (partials)
+    del w
+    x8 = torch.randn(8, 14336, device=gpu)
+    x16 = torch.randn(16, 14336, device=gpu)             # 16 slices of 16 rows: larger workspace
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.inference_mode(), torch.cuda.stream(s):
+        ref = quantized_linear(x8, q).clone()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            out = quantized_linear(x8, q)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            big = quantized_linear(x16, q)               # same stream, larger workspace
+            filler = torch.full((8 << 20,), 7.0, device=gpu)
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            print(f"[graph workspace replay {rep}]", flush=True)
+            assert torch.equal(out, ref), rep
+            assert bool((filler == 7.0).all()), rep
+            assert torch.isfinite(big).all()
+            del big, filler

@@ -332,3 +332,41 @@ def test_fused_projections_match_parts(gpu, scheme, m):
         _compare(o, y64, mag, f"fused part {scheme} m={m} n={w.shape[0]}")
         sep = q(x)
         assert torch.allclose(o, sep, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("scheme", ["int8", "int4"])
+def test_operand_checks_before_launch(gpu, scheme):
+    """Operands the kernels cannot read as given are converted or refused on
+    the host, before any launch: a bias or scales left on the CPU raise
+    RuntimeError (as F.linear does for mixed devices), float32 scales that
+    fp16 holds exactly and a non-contiguous payload give the same result,
+    inexact float32 scales raise QuantizationError."""
+    from kshipra_amd.quantization import QuantizationError, QuantizedWeight
+    n, k = 96, 256
+    w = gaussian((n, k), seed=77)
+    wt = torch.from_numpy(w).to(gpu)
+    qw = quantize_int8_per_channel(wt) if scheme == "int8" else quantize_int4_per_group(wt, 128)
+    x = torch.from_numpy(gaussian((3, k), seed=78, std=1.0)).to(gpu)
+    b = torch.from_numpy(gaussian((n,), seed=79)).to(gpu)
+    ref = quantized_linear(x, qw, b)
+    with pytest.raises(RuntimeError):
+        quantized_linear(x, qw, b.cpu())
+    with pytest.raises(RuntimeError):
+        quantized_linear(x, QuantizedWeight(qw.payload, qw.scales.cpu(), qw.scheme, qw.original_shape,
+                                            qw.group_size, qw.in_features_padded), b)
+    s32 = QuantizedWeight(qw.payload, qw.scales.float(), qw.scheme, qw.original_shape,
+                          qw.group_size, qw.in_features_padded)
+    assert torch.equal(quantized_linear(x, s32, b), ref)
+    bad = QuantizedWeight(qw.payload, qw.scales.float() * (1 + 2 ** -20), qw.scheme,
+                          qw.original_shape, qw.group_size, qw.in_features_padded)
+    with pytest.raises(QuantizationError):
+        quantized_linear(x, bad, b)
+    strided = qw.payload.t().contiguous().t()                  # same values, column-major
+    assert not strided.is_contiguous()
+    nc = QuantizedWeight(strided, qw.scales, qw.scheme, qw.original_shape, qw.group_size,
+                         qw.in_features_padded)
+    assert torch.equal(quantized_linear(x, nc, b), ref)
+    lin = nn.Linear(k, n, device=gpu)
+    ql = QuantizedLinear(lin, scheme).cpu()                     # moves the bias buffer only
+    with pytest.raises(RuntimeError):
+        ql(x)
