@@ -76,6 +76,16 @@ def rope_cos_sin(head_dim: int, positions: np.ndarray, theta: float):
     return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
 
 
+def expand_kv(kv: np.ndarray, g: int) -> np.ndarray:
+    """GQA: query head h reads KV head h // g (engine/chunked_prefill.py:104-105)."""
+    return np.repeat(kv, g, axis=0)
+
+
+def future_mask(qpos: np.ndarray, s: int) -> np.ndarray:
+    """True where key position > query position (causal, engine/chunked_prefill.py:122-126)."""
+    return np.arange(s)[None, :] > qpos[:, None]
+
+
 def apply_rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     """engine/model.py:30-32, 47-55.  x: [H, L, D]; cos/sin: [L, D]."""
     half = x.shape[-1] // 2
@@ -132,12 +142,10 @@ class OracleDecoder:
             vc = v if self.v_cache[li] is None else np.concatenate([self.v_cache[li], v], axis=1)
             self.k_cache[li], self.v_cache[li] = kc, vc
             S = kc.shape[1]
-            kq = np.repeat(kc, g, axis=0)
-            vq = np.repeat(vc, g, axis=0)
+            kq = expand_kv(kc, g)
+            vq = expand_kv(vc, g)
             s = np.matmul(q, kq.transpose(0, 2, 1)) * scale                # [H, L, S]
-            qpos = pos[:, None]
-            kpos = np.arange(S)[None, :]
-            s = np.where(kpos > qpos, np.float32(-np.inf), s)
+            s = np.where(future_mask(pos, S), np.float32(-np.inf), s)
             s = s - s.max(axis=-1, keepdims=True)
             p = np.exp(s)
             p = p / p.sum(axis=-1, keepdims=True)
