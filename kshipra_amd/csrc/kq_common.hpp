@@ -231,8 +231,8 @@ __device__ __forceinline__ floatx4 mfma16x16x32(half8_t a, half8_t b, floatx4 c)
 //
 // Non-finite entries: the maximum is taken over |x| with NaN ignored and is
 // clamped to FLT_MAX, so a row holding +-inf keeps its finite entries in
-// range; +-inf itself becomes hi = +-inf, lo = 0 (products inf * q give +-inf,
-// or NaN for q = 0, as the fp32 product does); NaN stays NaN.
+// range; +-inf itself becomes hi = +-inf, lo = 0 (products inf * q give
+// +-inf, or NaN for q = 0, as the fp32 product does); NaN stays NaN.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float absmax8(const float (&v)[8], float m) {
 #pragma unroll
@@ -256,7 +256,10 @@ __device__ __forceinline__ void split_hi_lo(const float (&v)[8], int e, half8_t&
     const _Float16 h = (_Float16)t;
     const float d = t - (float)h;
     hi[s] = h;
-    lo[s] = (_Float16)(d == d ? d : 0.0f);   // +-inf: inf - inf = NaN -> 0
+    // +-inf: inf - inf = NaN -> 0.  (lo must be 0, not merely finite: a
+    // large finite lo-row sum scaled back by 2^-e could itself overflow and
+    // meet hi's inf with the opposite sign.)
+    lo[s] = (_Float16)(d == d ? d : 0.0f);
   }
 }
 

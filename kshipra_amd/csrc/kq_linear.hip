@@ -299,8 +299,7 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     int64_t ng, int64_t nunits, int64_t per_wave, int pitch, const half8_t* __restrict__ xa,
     const int* __restrict__ xexp, const float* __restrict__ bias, float* __restrict__ y,
     int64_t ldy, int64_t N,
-    int2* __restrict__ argp, int pairs, int64_t split_units, int64_t split_ystride,
-    int* __restrict__ pexp) {
+    int2* __restrict__ argp, int pairs, int64_t split_units, int64_t split_ystride) {
   static_assert(!M1 || (A_LDS && HL && !REM), "single-row instances stage in LDS, pre-loads only");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int TPU = BITS == 4 ? 4 : 2;  // k-steps per unit
@@ -592,61 +591,47 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 
   // Cross-wave reduction in a fixed order.  Lane (qd, c) holds output-tile
   // rows 4qd+i, column c of each tile (HL: row m is the hi part of x[m], row
-  // m + 8 its lo part), in its wave's scaled domain: 2^e_w[m] times the true
-  // sum, e_w[m] the wave's exponent of row m (staged in LDS: held by the
-  // lanes of row m; staged by the pre-pass: one exponent per row, xexp).
-  // The waves' sums of a row meet in the domain of the row's smallest
-  // exponent E (each term scaled by 2^(E - e_w) <= 1, exact unless it is
-  // negligible) and are scaled back by 2^-E once, so an output in the fp32
-  // subnormal range is rounded once.  With a K split the slice writes its
-  // sum still scaled, with E in pexp[slice * M + m], for the ordered
-  // reduction to combine.
-  float* red = reinterpret_cast<float*>(smem);
-  int* sh_e;
-  {
-    const int red_bytes = nwaves * NT * 256 * 4;
-    const int stage_bytes = A_LDS ? 128 * pitch * M : 0;
-    sh_e = reinterpret_cast<int*>(smem + (red_bytes > stage_bytes ? red_bytes : stage_bytes));
-  }
-  if constexpr (A_LDS) {
-    if (sub == 0 && row_lane) sh_e[wave * 16 + my_m] = ex;
-  } else {
-    if (lane < M) sh_e[wave * 16 + lane] = xexp[lane];
+  // m + 8 its lo part), scaled by 2^e_w[m], the wave's exponent of row m
+  // (staged in LDS: held by the lanes of row m; staged by the pre-pass: one
+  // exponent per row, xexp).  Each wave scales its sums back before the
+  // cross-wave sum.  That is exact unless a wave's partial sum lies in the
+  // fp32 subnormal range (an output below 2^-126), where each wave's (and
+  // each K slice's) partial is rounded once, 2^-150 at most.
+  int erow[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 4 * qd + i;
+    int mr = HL ? (r < 8 ? r : r - 8) : r;
+    mr = mr < M ? mr : M - 1;
+    if constexpr (A_LDS) erow[i] = (M1 || lpr == 64) ? ex : __shfl(ex, mr * lpr, 64);
+    else erow[i] = xexp[mr];
   }
   __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) red[((wave * NT + t) * 16 + 4 * qd + i) * 16 + c] = acc[t][i];
+    for (int i = 0; i < 4; i++)
+      red[((wave * NT + t) * 16 + 4 * qd + i) * 16 + c] = unscale(acc[t][i], erow[i]);
   __syncthreads();
-  const bool split = !M1 && gridDim.y > 1;
-  // Row m's common exponent and the sum over waves of tile t, column cc.
-  auto row_exp = [&](int m) {
-    int e = sh_e[m];
-    for (int w = 1; w < nwaves; w++) e = min(e, sh_e[w * 16 + m]);
-    return e;
-  };
-  auto wave_sum = [&](int t, int m, int cc, int e) {
-    float v = 0.0f;
-    for (int w = 0; w < nwaves; w++) {
-      const int d = e - sh_e[w * 16 + m];
-      v += __builtin_amdgcn_ldexpf(red[((w * NT + t) * 16 + m) * 16 + cc], d);
-      if constexpr (HL) v += __builtin_amdgcn_ldexpf(red[((w * NT + t) * 16 + m + 8) * 16 + cc], d);
-    }
-    return v;
-  };
   // Gate / up pairs (NT == 2, weights interleaved by 16-row tiles): tile 0
   // holds gate rows, tile 1 the up rows of the same 16 output columns;
-  // y[m][16 b + c] = silu(g) * up.  (Never K-split.)
+  // y[m][16 b + c] = silu(g) * up.
   if constexpr (NT == 2) {
     if (pairs) {
       for (int o = tid; o < M * 16; o += blockDim.x) {
         const int m = o >> 4, cc = o & 15;
         const int64_t ngate = ncol0 + cc, nup = ngate + 16;
         if (nup < N) {
-          const int e = row_exp(m);
-          float g = unscale(wave_sum(0, m, cc, e), e);
-          float u = unscale(wave_sum(1, m, cc, e), e);
+          float g = 0.0f, u = 0.0f;
+          for (int w = 0; w < nwaves; w++) {
+            g += red[((w * NT) * 16 + m) * 16 + cc];
+            u += red[((w * NT + 1) * 16 + m) * 16 + cc];
+            if constexpr (HL) {
+              g += red[((w * NT) * 16 + m + 8) * 16 + cc];
+              u += red[((w * NT + 1) * 16 + m + 8) * 16 + cc];
+            }
+          }
           if constexpr (BITS == 8) { g *= f16_bits_to_f32(sc[ngate]); u *= f16_bits_to_f32(sc[nup]); }
           if (bias) { g += bias[ngate]; u += bias[nup]; }
           y[m * ldy + (int64_t)blockIdx.x * 16 + cc] = g / (1.0f + expf(-g)) * u;
@@ -665,15 +650,11 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
     float v = -__builtin_inff();
     int vi = 0x7fffffff;
     if (nn < N) {
-      const int e = row_exp(m);
-      v = wave_sum(t, m, cc, e);
-      if (split) {
-        if constexpr (BITS == 8) v *= f16_bits_to_f32(sc[nn]);
-        y[m * ldy + nn] = v;                       // partial, still scaled by 2^e
-        if (nn == ncol0) pexp[(int64_t)blockIdx.y * M + m] = e;
-        continue;
+      v = 0.0f;
+      for (int w = 0; w < nwaves; w++) {
+        v += red[((w * NT + t) * 16 + m) * 16 + cc];
+        if constexpr (HL) v += red[((w * NT + t) * 16 + m + 8) * 16 + cc];
       }
-      v = unscale(v, e);
       if constexpr (BITS == 8) v *= f16_bits_to_f32(sc[nn]);
       if (bias) v += bias[nn];
       if (y) y[m * ldy + nn] = v;
@@ -766,6 +747,9 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
   gemm_tile(tiles_m, tiles_n, gm, tm, tn, z);
   const int64_t m0 = tm * BM;
   const int64_t n0 = (tn * WN + wave) * (16 * NTW);
+  // Lane l holds the exponent of row m0 + l (BM <= 64), loaded now so the
+  // epilogue reads it with a lane shuffle instead of a memory round trip.
+  const int lane_exp = rexp[m0 + (lane < BM ? lane : 0)];
   const int64_t sb = z * spz;
   const int64_t se = sb + spz < nstages ? sb + spz : nstages;
 
@@ -899,7 +883,7 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
 #pragma unroll
   for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) er[mt][i] = rexp[m0 + mt * 16 + 4 * qd + i];
+    for (int i = 0; i < 4; i++) er[mt][i] = __shfl(lane_exp, mt * 16 + 4 * qd + i, 64);
 #pragma unroll
   for (int t = 0; t < NTW; t++) {
     const int64_t n = n0 + t * 16 + c;
@@ -990,6 +974,9 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
   gemm_tile(tiles_m, tiles_n, gm, tm, tn, z);
   const int64_t m0 = tm * BM;
   const int64_t nb = tn * NC * 16 * NTW;                // first column of the workgroup
+  // Lane l holds the exponent of row m0 + l (BM = 64), loaded now so the
+  // epilogue reads it with a lane shuffle instead of a memory round trip.
+  const int lane_exp = rexp[m0 + lane];
   const int64_t sb = z * spz;
   const int64_t se = sb + spz < nstages ? sb + spz : nstages;
   const int64_t nst = se - sb;
@@ -1114,7 +1101,7 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
 #pragma unroll
   for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) er[mt][i] = rexp[m0 + mt * 16 + 4 * qd + i];
+    for (int i = 0; i < 4; i++) er[mt][i] = __shfl(lane_exp, mt * 16 + 4 * qd + i, 64);
 #pragma unroll
   for (int t = 0; t < NTW; t++) {
     const int64_t n = n0 + t * 16 + c;
@@ -1218,8 +1205,9 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const int2* __restri
 
 // y[m, n] = (sum over z of part[z, m, n]) (* INT8 row scale) + bias, z in
 // order.  Partial z of row m is scaled by 2^pexp[z * pz + m] (pz = 0: one
-// exponent per row for every slice); the slices meet in the domain of the
-// row's smallest exponent E and the sum is scaled back by 2^-E once.
+// exponent per row for every slice; pexp null: unscaled partials); the
+// slices meet in the domain of the row's smallest exponent E and the sum is
+// scaled back by 2^-E once.
 // VEC: four consecutive n per thread (N % 4 == 0, y rows 16-byte aligned).
 template <int BITS, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S,
@@ -1233,7 +1221,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   for (int64_t o = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V; o < total;
        o += (int64_t)gridDim.x * blockDim.x * V) {
     const int64_t m = o / N, n = o - m * N;
-    int e = pexp[m];
+    int e = pexp ? pexp[m] : 0;
     for (int zz = 1; zz < S && pz != 0; zz++) e = min(e, pexp[zz * pz + m]);
     float v[V];
 #pragma unroll
@@ -1536,8 +1524,7 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
     if (!p.a_lds) p.pitch = p.nT;
     // Pre-pass staging: the staged rows, then one scale exponent per row.
     p.ws = p.a_lds ? 0 : align256((size_t)(128 * p.pitch * m)) + (size_t)(4 * m);
-    // K split: partials, then their exponents (staging is in LDS)
-    if (p.ksplit > 1) p.ws = align256((size_t)(4 * p.ksplit * m * n)) + (size_t)(4 * p.ksplit * m);
+    if (p.ksplit > 1) p.ws = (size_t)(4 * p.ksplit * m * n);   // partials (staging is in LDS)
     return p;
   }
   const int64_t keff = p.nT * 32;
@@ -1596,12 +1583,12 @@ void launch_skinny_ks(const Plan& p, dim3 grid, dim3 block, size_t shm, hipStrea
                       const float* x, int64_t ldx, int64_t m, int64_t k, bool xvec,
                       const uint8_t* wq, const uint16_t* sc, int64_t row_bytes, int64_t ng,
                       const half8_t* xa, const int* xexp, const float* bias, float* y,
-                      int64_t ldy, int64_t n, int2* argp, int* pexp) {
+                      int64_t ldy, int64_t n, int2* argp) {
   const int pairs = p.pairs ? 1 : 0;
 #define KQ_SKINNY(KS_, NT_)                                                                   \
   skinny_kernel<BITS, KS_, NT_, LDS, HL, SVEC, M1, REM><<<grid, block, shm, st>>>(            \
       x, ldx, (int)m, k, xvec, wq, sc, row_bytes, ng, p.nunits, p.per_wave, (int)p.pitch, xa, \
-      xexp, bias, y, ldy, n, argp, pairs, p.split_units, m * n, pexp)
+      xexp, bias, y, ldy, n, argp, pairs, p.split_units, m * n)
   if (p.nt == 4) {
     if (p.ks == 2) KQ_SKINNY(2, 4); else KQ_SKINNY(4, 4);
   } else if (p.nt == 2) {
@@ -1642,19 +1629,17 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
   }
   const size_t red = (size_t)p.waves * p.nt * 256 * sizeof(float);
   const size_t abytes = p.a_lds ? (size_t)(128 * p.pitch * m) : 0;
-  const size_t shm = std::max(red, abytes) + (size_t)p.waves * 16 * sizeof(int);  // + row exponents
+  const size_t shm = std::max(red, abytes);
   const dim3 grid((unsigned)((n + 16 * p.nt - 1) / (16 * p.nt)), (unsigned)p.ksplit);
   // K split: the slices write partials (row scale applied, no bias) to the
   // workspace, [slice][m][n]; the reduction adds them in slice order + bias.
   float* const y_out = y;
   const int64_t ldy_out = ldy;
   const float* const bias_out = bias;
-  int* pexp = nullptr;
   if (p.ksplit > 1) {
     y = static_cast<float*>(ws);
     ldy = n;
     bias = nullptr;
-    pexp = reinterpret_cast<int*>(static_cast<char*>(ws) + align256((size_t)(4 * p.ksplit * m * n)));
   }
   const dim3 block((unsigned)(64 * p.waves));
   const bool svec = p.svec && reinterpret_cast<uintptr_t>(sc) % (2 * p.ks) == 0;
@@ -1663,11 +1648,11 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
     if (svec)                                                                                   \
       launch_skinny_ks<BITS, LDS_, HL_, true, M1_, REM_>(p, grid, block, shm, st, x, ldx, m, k, \
                                                          xvec, wq, sc, row_bytes, ng, xa, xexp, \
-                                                         bias, y, ldy, n, argp, pexp);          \
+                                                         bias, y, ldy, n, argp);                \
     else                                                                                        \
       launch_skinny_ks<BITS, LDS_, HL_, false, M1_, REM_>(p, grid, block, shm, st, x, ldx, m,   \
                                                           k, xvec, wq, sc, row_bytes, ng, xa,   \
-                                                          xexp, bias, y, ldy, n, argp, pexp);   \
+                                                          xexp, bias, y, ldy, n, argp);         \
   } while (0)
   // Do the pre-loads (one batch of KS units at M = 1, else 4 entries per
   // lane over all rows) cover every activation entry of every wave?  The
@@ -1704,8 +1689,8 @@ int launch_skinny(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t
     const int64_t items = vec ? m * n / 4 : m * n;
     const unsigned rg = (unsigned)std::min<int64_t>((items + 255) / 256, 8192);
     // BITS = 4 instance: sums only (the slices applied any INT8 row scale)
-    if (vec) splitk_reduce_kernel<4, true><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, pexp, m, nullptr, bias_out, y_out, ldy_out);
-    else splitk_reduce_kernel<4, false><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, pexp, m, nullptr, bias_out, y_out, ldy_out);
+    if (vec) splitk_reduce_kernel<4, true><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, nullptr, 0, nullptr, bias_out, y_out, ldy_out);
+    else splitk_reduce_kernel<4, false><<<rg, 256, 0, st>>>(y, (int)p.ksplit, m, n, nullptr, 0, nullptr, bias_out, y_out, ldy_out);
   }
   return kq_check_launch(BITS == 4 ? "kq_linear_int4 (skinny)" : "kq_linear_int8 (skinny)");
 }

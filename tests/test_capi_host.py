@@ -53,11 +53,10 @@ def test_workspace_query_is_host_only():
     assert lib.kq_linear_workspace_bytes(8, 8, 4096, 4096, 0) == 0
     assert lib.kq_linear_workspace_bytes(8, 8, 28672, 4096, 0) == 4 * 8 * 4096 + 4 * 8
     # K = 14336, M >= 3: K split into slices staged in LDS; the workspace
-    # holds one fp32 partial output per slice (8 slices at M = 8, 4 at M = 4
-    # and 3), then one scale exponent per (slice, row)
-    assert lib.kq_linear_workspace_bytes(4, 8, 4096, 14336, 128) == 8 * 4 * 8 * 4096 + 4 * 8 * 8
-    assert lib.kq_linear_workspace_bytes(8, 4, 4096, 14336, 0) == 4 * 4 * 4 * 4096 + 4 * 4 * 4
-    assert lib.kq_linear_workspace_bytes(8, 3, 4096, 14336, 0) == 4 * 4 * 3 * 4096 + 4 * 4 * 3
+    # holds one fp32 partial output per slice (8 slices at M = 8, 4 at M = 4 and 3)
+    assert lib.kq_linear_workspace_bytes(4, 8, 4096, 14336, 128) == 8 * 4 * 8 * 4096
+    assert lib.kq_linear_workspace_bytes(8, 4, 4096, 14336, 0) == 4 * 4 * 4 * 4096
+    assert lib.kq_linear_workspace_bytes(8, 3, 4096, 14336, 0) == 4 * 4 * 3 * 4096
     # ... below M = 3, whole-K workgroups stage x in LDS: no workspace
     assert lib.kq_linear_workspace_bytes(4, 2, 4096, 14336, 128) == 0
     # GEMM path: operand planes for M rounded up to the 64-row tile, then one

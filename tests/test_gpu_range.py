@@ -79,9 +79,12 @@ def _check(y: np.ndarray, x: np.ndarray, w_hat: np.ndarray, label: str):
     mag = np.abs(x64) @ np.abs(w_hat).T
     y = y.astype(np.float64).reshape(y64.shape)
     assert np.isfinite(y).all(), f"{label}: non-finite output where the reference is finite"
-    # fp32 cannot hold an output below 2^-126 to 1e-4 relative: allow two
-    # roundings at the subnormal spacing (2^-149 each) on top of the bars.
-    err = np.maximum(np.abs(y - y64) - 2.0 ** -148, 0.0)
+    # fp32 cannot hold an output below 2^-126 to 1e-4 relative.  There the
+    # kernels round each wave's and each K slice's partial sum once (at most
+    # 16 waves + 16 slices + the output), 2^-150 each: allow 2^-144 absolute
+    # on top of the bars (the fp32 reference rounds every one of its K
+    # products at that spacing).
+    err = np.maximum(np.abs(y - y64) - 2.0 ** -144, 0.0)
     # norm-wise per row: rows of very different magnitude are each held to the bar
     rmax = np.maximum(np.abs(y64).max(axis=1, keepdims=True), 1e-300)
     norm = (err / rmax)[np.abs(y64).max(axis=1) > 0].max(initial=0.0)
