@@ -100,6 +100,23 @@ int kq_linear_int4(const float* x, int64_t m, int64_t ldx, const uint8_t* payloa
                    const float* bias, float* y, int64_t ldy, int64_t n, int64_t k,
                    void* workspace, size_t workspace_bytes, kq_stream_t stream);
 
+/* Device scratch the no-allocation entry point below holds per GPU. */
+#define KQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): kq_linear_int4 with the same arguments and results, but
+ * no workspace argument -- the scratch it needs (at most
+ * KQ_NOALLOC_SCRATCH_BYTES; larger shapes return KQ_ERR_WORKSPACE without
+ * launching) is a static device array of the library, one per GPU, held
+ * until the process ends.  Calls nothing that allocates.  Call it with the
+ * stream's device current.  Calls that overlap on one GPU share that array
+ * and race: order them on one stream or synchronise between them. */
+int kq_linear_int4_noalloc(const float* x, int64_t m, int64_t ldx, const uint8_t* payload,
+                           const uint16_t* scales, int64_t group_size, int64_t k_padded,
+                           const float* bias, float* y, int64_t ldy, int64_t n, int64_t k,
+                           kq_stream_t stream);
+
 /* Workspace bytes for kq_linear_argmax_int8 / _int4 with these sizes (host
  * only; scheme 8 or 4). */
 size_t kq_linear_argmax_workspace_bytes(int scheme, int64_t m, int64_t n, int64_t k,

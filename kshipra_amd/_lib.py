@@ -37,6 +37,8 @@ SIGNATURES = [
     ("kq_linear_int8", _int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     ("kq_linear_int4", _int,
      [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    ("kq_linear_int4_noalloc", _int,
+     [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
     ("kq_linear_argmax_workspace_bytes", _sz, [_int, _i64, _i64, _i64, _i64]),
     ("kq_linear_argmax_int8", _int,
      [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
