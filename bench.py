@@ -23,12 +23,13 @@ Also reported (same JSON line):
   * ``roofline``: the kernel that dominates the headline step (the fused
     gate/up dequant-GEMV, [28672 x 4096]) vs the 8 TB/s HBM peak, with its
     HBM traffic from the rocprofv3 counter summary under profiles/;
-  * ``cpu_baseline``: the oracle's restatement of the reference forward
-    (materialise w_hat = q * s in fp32, then one fp32 BLAS GEMV) timed on this
-    host's cores over one layer (7 projections).
+  * ``cpu_baseline``: the reference's CPU forward (torch materialises the
+    fp32 weight, then F.linear; oracle/torch_ref.py) on this host with all
+    available physical cores and with one thread, one row per config (large
+    ones on a stated sample); ``value`` is the INT4 M = 1 Llama-3-8B layer.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--eager] [--quick]
-                       [--only all|prefill|lm_head|attention]
+                       [--only all|prefill|lm_head|attention|batch|cpu]
 """
 
 from __future__ import annotations
@@ -339,55 +340,135 @@ def attention(dev, steps, warmup, eager):
     return out
 
 
-def cpu_baseline(layer, budget_s=20.0):
-    """The oracle's restatement of QuantizedLinear.forward (materialise the fp32
-    weight, then fp32 BLAS), on this host's cores, over one layer at M = 1."""
-    from oracle import quant
+def _host_info():
+    """CPU model, logical CPUs, the CPUs this process may run on and how many
+    distinct physical cores those are (from the sysfs topology)."""
+    info = {"os_cpu_count": os.cpu_count()}
     try:
-        from threadpoolctl import threadpool_limits, threadpool_info
-        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()
-                            if i.get("user_api") == "blas"] or [1])
-    except Exception:                                # threadpoolctl absent: report the default
-        threadpool_limits, blas_threads = None, None
-    host = []
-    for name, n, k in SHAPES:
-        p = layer[name]
-        host.append((p.qw.payload.cpu().numpy(), p.qw.scales.cpu().numpy(), n, k,
-                     np.random.default_rng(0).standard_normal((1, k)).astype(np.float32)))
-    nbytes = sum(algorithmic_bytes(1, n, k, "int4") for _, _, n, k, _ in host)
+        cpus = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        cpus = list(range(os.cpu_count() or 1))
+    info["affinity_cpus"] = len(cpus)
+    cores = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            pkg = open(base + "physical_package_id").read().strip()
+            core = open(base + "core_id").read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    info["physical_cores"] = len(cores)
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return info
 
-    def one_pass():
-        for payload, scales, n, k, x in host:
-            w_hat = quant.np_dequantize_int4(payload, scales, k, 128)
-            quant.linear_f32(x, w_hat)
 
-    one_pass()                                       # warm-up
+def _time_cpu(fn, budget_s, max_iter=5, warmup=1):
+    """Median wall time (s) of fn() after warm-up, at most max_iter runs and
+    roughly budget_s seconds."""
+    for _ in range(warmup):
+        fn()
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+    while len(times) < max_iter and (not times or time.perf_counter() - t_start < budget_s):
         t0 = time.perf_counter()
-        one_pass()
+        fn()
         times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
-    cores = blas_threads or os.cpu_count()
-    # The same with one BLAS thread (the reference harness pins one thread).
-    t1 = None
-    if threadpool_limits is not None:
-        with threadpool_limits(limits=1, user_api="blas"):
-            one_pass()
-            t1s = []
-            for _ in range(2):
-                t0 = time.perf_counter()
-                one_pass()
-                t1s.append(time.perf_counter() - t0)
-        t1 = float(np.median(t1s))
-    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": int(cores), "kind": "port",
-            "sample": (f"one Llama-3-8B layer (7 projections, INT4 G=128, M=1): numpy "
-                       f"dequantize (1 thread) + OpenBLAS fp32 GEMV ({cores} threads); median of "
-                       f"{len(times)} passes, {t * 1e3:.1f} ms/layer; host {os.cpu_count()} CPUs"),
-            "ms_per_layer": t * 1e3,
-            "value_1_thread": None if t1 is None else nbytes / t1 / 1e9,
-            "ms_per_layer_1_thread": None if t1 is None else t1 * 1e3}
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(dev, budget_s=40.0):
+    """The reference's CPU forward (oracle/torch_ref.py: torch materialises the
+    fp32 weight, then F.linear; engine/quantization.py:226-230, 321-344,
+    394-396) on this host, for each BASELINE config, with all available
+    physical cores and with one thread (the reference harness's setting,
+    benchmarks/run_benchmarks.py:63,123).  Weights are quantized on the GPU
+    (bit-identical to the reference quantizer) and copied to host memory.
+    Large configs are timed on a stated sample (a number of layers or a row
+    slice of the weight) and reported as rates of that sample."""
+    import torch.nn.functional as F
+
+    from oracle import torch_ref
+    host = _host_info()
+    threads_all = max(1, host["physical_cores"])
+    g = torch.Generator(device=dev).manual_seed(21)
+
+    def q_host(n, k, scheme):
+        w = torch.randn(n, k, device=dev, generator=g) * 0.02
+        qw = quantize_int8_per_channel(w) if scheme == "int8" else quantize_int4_per_group(w, 128)
+        return qw.payload.cpu(), qw.scales.cpu()
+
+    rows = []
+    per_row_budget = budget_s / 12
+
+    def run(config, sample, projs, m, scheme, scale_rows=1.0, gflop=None):
+        """projs: [(payload, scales, n, k)] on the host; times one pass over them."""
+        xs = {k: torch.randn(m, k) for (_, _, _, k) in projs}
+        nbytes = sum(algorithmic_bytes(m, n, k, scheme) for (_, _, n, k) in projs)
+
+        def one():
+            for payload, scales, n, k in projs:
+                torch_ref.linear(xs[k], payload, scales, scheme, k)
+        for threads in (threads_all, 1):
+            torch.set_num_threads(threads)
+            t, it = _time_cpu(one, per_row_budget, max_iter=5 if threads > 1 else 3)
+            # rates over the sample (a row slice or a few layers runs at the
+            # rate of the whole); ms_full scales the sample's time up
+            r = {"config": config, "sample": sample, "threads": threads, "ms": round(t * 1e3, 2),
+                 "ms_full": round(t * 1e3 * scale_rows, 2), "iters": it,
+                 "gbs": round(nbytes / t / 1e9, 3)}
+            if gflop is not None:
+                r["tflops"] = round(gflop / t / 1e3, 4)
+            rows.append(r)
+            print(f"# cpu {config} {threads} threads: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
+
+    # 1. INT8 [4864 x 896] dequant-matvec
+    p, sc = q_host(4864, 896, "int8")
+    run("int8_4864x896_m1", "the whole config", [(p, sc, 4864, 896)], 1, "int8")
+    # 2. INT4 Qwen2.5-0.5B decode step: 2 of 24 layers (7 projections each)
+    qw = [q_host(n, k, "int4") + (n, k) for _ in range(2) for _, n, k in QWEN_SHAPES]
+    run("int4_qwen2.5_0.5b_step_m1", "2 of 24 layers", qw, 1, "int4", scale_rows=12.0)
+    # headline workload: INT4 Llama-3-8B decode step at M = 1, one layer
+    l4 = [q_host(n, k, "int4") + (n, k) for _, n, k in SHAPES]
+    run("int4_llama3_8b_step_m1", "1 of 32 layers (7 projections)", l4, 1, "int4", scale_rows=32.0)
+    del l4
+    # 3. INT8 Llama-3-8B layer at M = 1 / 8 / 32 / 64
+    l8 = [q_host(n, k, "int8") + (n, k) for _, n, k in SHAPES]
+    for m in (1, 8, 32, 64):
+        run(f"int8_llama3_8b_layer_m{m}", "one layer (7 projections)", l8, m, "int8",
+            gflop=2 * m * sum(n * k for _, _, n, k in l8) / 1e9)
+    del l8
+    # 4. INT4 prefill MLP, M = 512: gate and up [14336 x 4096], down [4096 x
+    #    14336] -- a quarter of each weight's rows (the work is row-separable)
+    mlp = []
+    for n, k in ((14336, 4096), (14336, 4096), (4096, 14336)):
+        pp, ss = q_host(n, k, "int4")
+        mlp.append((pp[: n // 4].contiguous(), ss[: n // 4].contiguous(), n // 4, k))
+    run("int4_prefill_mlp_m512", "a quarter of each weight's rows",
+        mlp, 512, "int4", scale_rows=4.0, gflop=2 * 512 * sum(n * k for _, _, n, k in mlp) / 1e9)
+    del mlp
+    # 5. lm_head [128256 x 4096] INT8 / INT4 at M = 1: an eighth of the vocab
+    for scheme in ("int8", "int4"):
+        pp, ss = q_host(128256, 4096, scheme)
+        part = [(pp[:16032].contiguous(), ss[:16032].contiguous(), 16032, 4096)]
+        del pp, ss
+        run(f"lm_head_{scheme}_m1", "an eighth of the vocabulary rows", part, 1, scheme,
+            scale_rows=8.0)
+    torch.set_num_threads(threads_all)
+    head = next(r for r in rows if r["config"] == "int4_llama3_8b_step_m1" and r["threads"] == threads_all)
+    head1 = next(r for r in rows if r["config"] == "int4_llama3_8b_step_m1" and r["threads"] == 1)
+    return {"value": head["gbs"], "unit": "GB/s", "cores": threads_all, "kind": "port",
+            "sample": (f"the reference's CPU forward (torch dequantize + F.linear, oracle/torch_ref.py) "
+                       f"over one Llama-3-8B layer (7 INT4 G=128 projections, M=1), {head['ms']} ms "
+                       f"with {threads_all} threads ({head1['ms']} ms with 1); every BASELINE config "
+                       f"is in rows"),
+            "host": host, "rows": rows}
 
 
 def main():
@@ -399,7 +480,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
     ap.add_argument("--layers", type=int, default=LAYERS,
                     help="layers in the sweep (fewer only for counter runs; the headline uses 32)")
-    ap.add_argument("--only", choices=("all", "prefill", "lm_head", "attention", "batch"), default="all",
+    ap.add_argument("--only", choices=("all", "prefill", "lm_head", "attention", "batch", "cpu"), default="all",
                     help="profiling aid: run one section and print its figures only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -416,6 +497,8 @@ def main():
             print(json.dumps({"section": "int4_prefill_m512_mlp", "tflops": round(pf["tflops"], 1),
                               "ms": round(pf["ms"], 4), "gflop": round(pf["gflop"], 1),
                               "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}))
+        elif args.only == "cpu":
+            print(json.dumps({"section": "cpu_baseline", "results": cpu_baseline(dev)}))
         elif args.only == "attention":
             print(json.dumps({"section": "attention_llama3_8b_heads",
                               "results": attention(dev, args.steps, args.warmup, args.eager)}))
@@ -499,7 +582,7 @@ def main():
                                               "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}
         breakdown["lm_head_128256x4096"] = lm_head(dev, args.steps, args.warmup, args.eager)
         breakdown["attention_llama3_8b_heads"] = attention(dev, max(args.steps // 2, 3), 1, args.eager)
-        cpu = cpu_baseline(int4[0])
+        cpu = cpu_baseline(dev)
 
     # a plain 1 GiB device copy: the reference point for HBM-traffic counters
     src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
