@@ -29,7 +29,7 @@ Also reported (same JSON line):
     ones on a stated sample); ``value`` is the INT4 M = 1 Llama-3-8B layer.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--eager] [--quick]
-                       [--only all|prefill|lm_head|attention|batch|cpu]
+                       [--only all|prefill|lm_head|attention|batch|cpu|m1]
 """
 
 from __future__ import annotations
@@ -192,6 +192,22 @@ def measure(layers, m, dev, steps, warmup, eager, names=None, shapes=None):
     ms = time_steps(sw.step, steps, warmup)
     return {"ms": ms, "bytes": sw.bytes, "flops": sw.flops,
             "gbs": sw.bytes / (ms * 1e-3) / 1e9, "tflops": sw.flops / (ms * 1e-3) / 1e12}
+
+
+def batch_steps(int8, int4, dev, steps, warmup, eager, ms):
+    """Continuous-batching decode steps at batch M: the 7 projections as
+    separate launches (``int8_m{M}``), and as the decoder runs them with
+    q/k/v and gate/up row-stacked (4 launches per layer, ``*_fused``)."""
+    out = {}
+    for m in ms:
+        for scheme, layers in (("int8", int8), ("int4", int4)):
+            r = measure(layers, m, dev, steps, warmup, eager)
+            out[f"{scheme}_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
+                                     "us_per_step": round(r["ms"] * 1e3, 1)}
+            r = measure(layers, m, dev, steps, warmup, eager, names=[f[0] for f in FUSED])
+            out[f"{scheme}_m{m}_fused"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
+                                           "us_per_step": round(r["ms"] * 1e3, 1)}
+    return out
 
 
 def prefill_tflops(dev, steps, warmup, eager):
@@ -480,7 +496,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extras, no CPU baseline)")
     ap.add_argument("--layers", type=int, default=LAYERS,
                     help="layers in the sweep (fewer only for counter runs; the headline uses 32)")
-    ap.add_argument("--only", choices=("all", "prefill", "lm_head", "attention", "batch", "cpu"), default="all",
+    ap.add_argument("--only", choices=("all", "prefill", "lm_head", "attention", "batch", "cpu", "m1"), default="all",
                     help="profiling aid: run one section and print its figures only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -497,22 +513,28 @@ def main():
             print(json.dumps({"section": "int4_prefill_m512_mlp", "tflops": round(pf["tflops"], 1),
                               "ms": round(pf["ms"], 4), "gflop": round(pf["gflop"], 1),
                               "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}))
+        elif args.only == "m1":
+            # M = 1 per projection, INT4 and INT8 (counter runs)
+            res = {}
+            for scheme, seed in (("int4", 1), ("int8", 2)):
+                layers = build_layers(scheme, dev, seed=seed, nlayers=args.layers)
+                for name, n, k in SHAPES + [f for f in FUSED if f[0] in ("qkv", "gate_up")]:
+                    r = measure(layers, 1, dev, args.steps, args.warmup, args.eager, names=[name])
+                    res[f"{scheme}_{name}"] = {"gbs": round(r["gbs"], 1),
+                                               "us_per_launch": round(r["ms"] * 1e3 / args.layers, 2)}
+                del layers
+                torch.cuda.empty_cache()
+            print(json.dumps({"section": "m1_per_projection", "results": res}))
         elif args.only == "cpu":
             print(json.dumps({"section": "cpu_baseline", "results": cpu_baseline(dev)}))
         elif args.only == "attention":
             print(json.dumps({"section": "attention_llama3_8b_heads",
                               "results": attention(dev, args.steps, args.warmup, args.eager)}))
         elif args.only == "batch":
-            # decode batches: the 7-projection step at M = 8, 32, 64
-            res = {}
-            for scheme, seed in (("int8", 2), ("int4", 1)):
-                layers = build_layers(scheme, dev, seed=seed, nlayers=args.layers)
-                for m in (8, 32, 64):
-                    r = measure(layers, m, dev, args.steps, args.warmup, args.eager)
-                    res[f"{scheme}_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
-                                             "us_per_step": round(r["ms"] * 1e3, 1)}
-                del layers
-                torch.cuda.empty_cache()
+            # decode batches: the 7-projection and the fused 4-launch step at M = 8, 32, 64
+            int8 = build_layers("int8", dev, seed=2, nlayers=args.layers)
+            int4 = build_layers("int4", dev, seed=1, nlayers=args.layers)
+            res = batch_steps(int8, int4, dev, args.steps, args.warmup, args.eager, (8, 32, 64))
             print(json.dumps({"section": "decode_batches_llama3_8b", "results": res}))
         else:
             print(json.dumps({"section": "lm_head_128256x4096",
@@ -567,13 +589,7 @@ def main():
             "gbs": round(rq["gbs"], 1), "us_per_step": round(rq["ms"] * 1e3, 1),
             "bytes_per_step": rq["bytes"], "launches": 4 * QWEN_LAYERS}
         del qwen
-        for m in (4, 8, 32, 64):
-            r = measure(int8, m, dev, max(args.steps // 2, 3), 1, args.eager)
-            breakdown[f"int8_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
-                                       "us_per_step": round(r["ms"] * 1e3, 1)}
-            r = measure(int4, m, dev, max(args.steps // 2, 3), 1, args.eager)
-            breakdown[f"int4_m{m}"] = {"gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 1),
-                                       "us_per_step": round(r["ms"] * 1e3, 1)}
+        breakdown.update(batch_steps(int8, int4, dev, max(args.steps // 2, 3), 1, args.eager, (4, 8, 32, 64)))
         del int8
         torch.cuda.empty_cache()
         pf = prefill_tflops(dev, max(args.steps // 2, 3), 1, args.eager)
