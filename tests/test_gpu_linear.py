@@ -370,3 +370,18 @@ def test_operand_checks_before_launch(gpu, scheme):
     ql = QuantizedLinear(lin, scheme).cpu()                     # moves the bias buffer only
     with pytest.raises(RuntimeError):
         ql(x)
+
+
+@pytest.mark.parametrize("n", [28672, 26000])
+def test_single_row_wide(gpu, n):
+    """INT4 M = 1 at the fused gate/up width [28672 x 4096] (more waves than
+    one round of the chip holds) and at a ragged N; aligned and unaligned
+    activations, bias."""
+    _run(gpu, 1, n, 4096, "int4", bias=True, seed=n)
+    w = gaussian((n, 4096), seed=n + 1)
+    qw = quantize_int4_per_group(torch.from_numpy(w).to(gpu), 128)
+    xs = torch.from_numpy(gaussian((1, 4097), seed=n + 2, std=1.0)).to(gpu)
+    y = quantized_linear(xs[:, 1:], qw)
+    torch.cuda.synchronize()
+    y64, mag = _reference(xs[:, 1:].cpu().numpy(), w, "int4", 128, None)
+    _compare(y, y64, mag, f"wide unaligned n={n}")

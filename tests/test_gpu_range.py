@@ -99,6 +99,7 @@ def _check(y: np.ndarray, x: np.ndarray, w_hat: np.ndarray, label: str):
 # through the workspace size where the library exposes it.
 CASES = [
     (1, 4096, 4096, "int4", True),      # single-row skinny instance
+    (1, 28672, 4096, "int4", True),     # single-row, wider than one round of waves
     (1, 4096, 4096, "int8", True),      # general skinny instance at M = 1
     (3, 1024, 4096, "int4", True),      # pre-loads cover every entry
     (8, 1024, 4096, "int8", False),     # remainder staging (unaligned x)
