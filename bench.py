@@ -487,6 +487,16 @@ def cpu_baseline(dev, budget_s=40.0):
             "host": host, "rows": rows}
 
 
+def hbm_copy_reference(dev):
+    """A plain 1 GiB device-to-device copy: the reference dispatch that scales
+    the FETCH_SIZE / WRITE_SIZE counters of the same run to HBM bytes."""
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -524,6 +534,7 @@ def main():
                                                "us_per_launch": round(r["ms"] * 1e3 / args.layers, 2)}
                 del layers
                 torch.cuda.empty_cache()
+            hbm_copy_reference(dev)
             print(json.dumps({"section": "m1_per_projection", "results": res}))
         elif args.only == "cpu":
             print(json.dumps({"section": "cpu_baseline", "results": cpu_baseline(dev)}))
@@ -600,11 +611,7 @@ def main():
         breakdown["attention_llama3_8b_heads"] = attention(dev, max(args.steps // 2, 3), 1, args.eager)
         cpu = cpu_baseline(dev)
 
-    # a plain 1 GiB device copy: the reference point for HBM-traffic counters
-    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    torch.cuda.synchronize()
+    hbm_copy_reference(dev)
 
     out = {
         "metric": "dequant-GEMV HBM GB/s (% of peak) at M=1 INT4/INT8; prefill GEMM TFLOPS",
