@@ -929,7 +929,11 @@ __global__ __launch_bounds__(64 * WN) void gemm_kernel(
 // 3-deep ring, or for INT4 grids that fill the GPU without a K split, 7
 // consumers (two math waves on most SIMDs, BN = 448) with a 2-deep ring
 // (measured 13 % faster there, slower elsewhere: partial 448-column tiles,
-// K splits).  INT8 windows need twice the weight ring: 4 consumers, 2 deep.
+// K splits).  INT8 windows need twice the weight ring: 4 consumers with split
+// producers (below), weights 3 deep, operands 2 deep -- measured 17-24 %
+// faster than one producer with a 2-deep ring at M = 96-512 on the Llama-3-8B
+// MLP shapes; for INT4 the deeper weight ring gains nothing (its consumers,
+// not the DMA, set the pace).
 constexpr int kWsNC = 4, kWsWideNC = 7;
 constexpr int64_t kWsWideMinTiles = 256;
 
@@ -947,8 +951,14 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
   __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
 
-template <int BITS, int D, int NC>
-__global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
+// DW > 0: two producer waves, each with its own memory counter -- one moves
+// the operand blocks through a 2-deep ring, the other the weights through a
+// DW-deep ring, DW - 1 stages ahead.  With one producer both streams share a
+// counter that retires in issue order, so waiting for the next operand block
+// also waits for every weight DMA issued before it, which caps the weights'
+// lead at about two stages whatever the ring depth.
+template <int BITS, int D, int NC, int DW = 0>
+__global__ __launch_bounds__(64 * (NC + (DW > 0 ? 2 : 1))) void gemm_ws_kernel(
     const half8_t* __restrict__ planes, int64_t Mp, int64_t M,
     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ sc, int64_t row_bytes,
     int64_t ng, int64_t nstages, int64_t spz, int tiles_m, int tiles_n, int gm,
@@ -959,15 +969,19 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
   constexpr int RAWN = BITS == 4 ? 1 : 2;               // 64-byte windows per stage
   constexpr int ABLK = 2 * PLANE / 64;                  // 1 KB operand blocks per stage
   constexpr int WBLK = NC * NTW * RAWN;                 // 1 KB weight blocks per stage
-  constexpr int SLOT = (ABLK + WBLK) * 64;              // 16-byte entries per slot
   constexpr int NDMA = ABLK + WBLK;                     // producer DMAs per stage
-  static_assert(NDMA * (D - 2) < 64, "vmcnt range");
-  static_assert(D * SLOT * 16 <= 160 * 1024, "LDS ring exceeds 160 KiB");
-  __shared__ u32x4 ring[D * SLOT];
+  constexpr bool SPLIT = DW > 0;
+  constexpr int DA = SPLIT ? 2 : D;                     // operand ring depth
+  constexpr int DWR = SPLIT ? DW : D;                   // weight ring depth
+  static_assert(SPLIT || NDMA * (D - 2) < 64, "vmcnt range");
+  static_assert(!SPLIT || WBLK * (DW - 2) < 64, "vmcnt range");
+  static_assert((DA * ABLK + DWR * WBLK) * 64 * 16 <= 160 * 1024, "LDS rings exceed 160 KiB");
+  __shared__ u32x4 aring[DA * ABLK * 64];
+  __shared__ u32x4 wring[DWR * WBLK * 64];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool producer = wave == NC;
+  const bool producer = wave >= NC;
   const int qd = lane >> 4, c = lane & 15;
 
   int64_t tm, tn, z;
@@ -983,14 +997,17 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
 
   // Producer addressing: operand block j -> plane j / (BM/4), rows 4 (j % (BM/4)) + (lane >> 4);
   // weight block (w, t, rr) -> row nb + 64 w + 16 t + (lane & 15), byte (lane >> 4) * 16.
-  auto issue = [&](int64_t st, int sl) {
-    u32x4* base = ring + sl * SLOT;
+  auto issue_a = [&](int64_t st, int sl) {
+    u32x4* base = aring + sl * ABLK * 64;
 #pragma unroll
     for (int j = 0; j < ABLK; j++) {
       const int p = j / (BM / 4), mm = (j % (BM / 4)) * 4 + (lane >> 4), ph = lane & 15;
       const int64_t e = ((p * nstages + st) * Mp + m0 + mm) * 16 + (ph ^ (mm & 15));
       dma16(planes + e, base + j * 64);
     }
+  };
+  auto issue_w = [&](int64_t st, int sl) {
+    u32x4* base = wring + sl * WBLK * 64;
 #pragma unroll
     for (int w = 0; w < NC; w++)
 #pragma unroll
@@ -999,7 +1016,7 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
         const uint8_t* src = wq + (n < N ? n : N - 1) * row_bytes + (lane >> 4) * 16;
 #pragma unroll
         for (int rr = 0; rr < RAWN; rr++)
-          dma16(src + (st * RAWN + rr) * 64, base + (ABLK + (w * NTW + t) * RAWN + rr) * 64);
+          dma16(src + (st * RAWN + rr) * 64, base + ((w * NTW + t) * RAWN + rr) * 64);
       }
   };
 
@@ -1019,13 +1036,38 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
   // Producer and consumers run separate loops with the same number of
   // barriers (one per stage), so neither path's registers burden the other.
   if (producer) {
+    if constexpr (SPLIT) {
+      if (wave == NC) {                           // operand blocks, one stage ahead
+        issue_a(sb, 0);
+        for (int64_t s = 0; s < nst; s++) {
+          wait_vmcnt<0>();                        // stage s has landed
+          __builtin_amdgcn_s_barrier();
+          const int64_t k = s + 1;                // into the slot read a stage ago
+          issue_a(sb + (k < nst ? k : nst - 1), (int)(k & 1));
+        }
+      } else {                                    // weights, DW - 1 stages ahead
 #pragma unroll
-    for (int k = 0; k < D - 1; k++) issue(sb + (k < nst ? k : nst - 1), k);
-    for (int64_t s = 0; s < nst; s++) {
-      wait_vmcnt<NDMA * (D - 2)>();               // stage s has landed
-      __builtin_amdgcn_s_barrier();
-      const int64_t k = s + D - 1;                // into the slot read a stage ago
-      issue(sb + (k < nst ? k : nst - 1), (int)(k % D));
+        for (int k = 0; k < DW - 1; k++) issue_w(sb + (k < nst ? k : nst - 1), k);
+        for (int64_t s = 0; s < nst; s++) {
+          wait_vmcnt<WBLK * (DW - 2)>();          // stage s has landed
+          __builtin_amdgcn_s_barrier();
+          const int64_t k = s + DW - 1;
+          issue_w(sb + (k < nst ? k : nst - 1), (int)(k % DW));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < D - 1; k++) {
+        issue_a(sb + (k < nst ? k : nst - 1), k);
+        issue_w(sb + (k < nst ? k : nst - 1), k);
+      }
+      for (int64_t s = 0; s < nst; s++) {
+        wait_vmcnt<NDMA * (D - 2)>();             // stage s has landed
+        __builtin_amdgcn_s_barrier();
+        const int64_t k = s + D - 1;              // into the slot read a stage ago
+        issue_a(sb + (k < nst ? k : nst - 1), (int)(k % D));
+        issue_w(sb + (k < nst ? k : nst - 1), (int)(k % D));
+      }
     }
     return;
   }
@@ -1044,14 +1086,14 @@ __global__ __launch_bounds__(64 * (NC + 1)) void gemm_ws_kernel(
 #pragma unroll
       for (int t = 0; t < NTW; t++) snx[t] = srow[t][sn];
     }
-    const u32x4* base = ring + (int)(s % D) * SLOT;
-    const half8_t* la = reinterpret_cast<const half8_t*>(base);
+    const u32x4* wbase = wring + (int)(s % DWR) * WBLK * 64;
+    const half8_t* la = reinterpret_cast<const half8_t*>(aring + (int)(s % DA) * ABLK * 64);
     u32x4 wr[NTW][RAWN];
 #pragma unroll
     for (int t = 0; t < NTW; t++)
 #pragma unroll
       for (int rr = 0; rr < RAWN; rr++)
-        wr[t][rr] = base[(ABLK + (wave * NTW + t) * RAWN + rr) * 64 + lane];
+        wr[t][rr] = wbase[((wave * NTW + t) * RAWN + rr) * 64 + lane];
     float sf[NTW];
     if constexpr (BITS == 4) {
 #pragma unroll
@@ -1387,6 +1429,7 @@ struct Plan {
   int64_t splits = 1;   // gemm: K splits (partials + ordered reduction when > 1)
   int gm = 1;           // gemm: m-tiles per band of the workgroup order
   int wsnc = 0;         // gemm: consumer waves of the warp-specialized kernel
+  bool wsdw = false;    // gemm: warp-specialized kernel with split producers (deep weight ring)
   bool pairs = false;   // skinny: gate / up tile pairs, silu(gate) * up epilogue
   int64_t mpad = 0;     // gemm: operand-plane rows (M rounded up to the row tile)
   bool wspec = false;   // gemm: warp-specialized DMA kernel (prefill chunks)
@@ -1536,6 +1579,7 @@ Plan make_plan(int bits, int64_t m, int64_t n, int64_t k, int64_t g, int64_t kp,
   if (p.wspec) {
     const int64_t wide = (n + 64 * kWsWideNC - 1) / (64 * kWsWideNC);
     p.wsnc = bits == 4 && p.tiles_m * wide >= kWsWideMinTiles ? kWsWideNC : kWsNC;
+    p.wsdw = bits == 8;
   }
   if (!p.wspec) {
     p.ntw = (n + 16 * 2 * kGemmWN - 1) / (16 * 2 * kGemmWN) <= kGemmNarrowMaxTiles ? 2 : 4;
@@ -1718,15 +1762,17 @@ int launch_gemm(const Plan& p, const float* x, int64_t ldx, int64_t m, int64_t k
   float* part = p.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + lay.part_off) : nullptr;
   if (p.wspec) {
     const unsigned blocks = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
-#define KQ_WS(D_, NC_)                                                                          \
-  gemm_ws_kernel<BITS, D_, NC_><<<blocks, 64 * (NC_ + 1), 0, st>>>(                            \
+#define KQ_WS(D_, NC_, DW_)                                                                     \
+  gemm_ws_kernel<BITS, D_, NC_, DW_><<<blocks, 64 * (NC_ + (DW_ > 0 ? 2 : 1)), 0, st>>>(        \
       planes, p.mpad, m, wq, sc, row_bytes, ng, p.nstages, p.spz, (int)p.tiles_m,               \
       (int)p.tiles_n, p.gm, rexp, bias, y, ldy, n, part)
     if constexpr (BITS == 4) {
-      if (p.wsnc == kWsWideNC) KQ_WS(2, kWsWideNC);
-      else KQ_WS(3, kWsNC);
+      if (p.wsdw) KQ_WS(2, kWsNC, 5);
+      else if (p.wsnc == kWsWideNC) KQ_WS(2, kWsWideNC, 0);
+      else KQ_WS(3, kWsNC, 0);
     } else {
-      KQ_WS(2, kWsNC);
+      if (p.wsdw) KQ_WS(2, kWsNC, 3);
+      else KQ_WS(2, kWsNC, 0);
     }
 #undef KQ_WS
   } else if (p.mtw == 2) {
