@@ -227,7 +227,9 @@ __device__ __forceinline__ floatx4 mfma16x16x32(half8_t a, half8_t b, floatx4 c)
 // range).  The representation error of an element is at most 2^-22 |x| (hi
 // keeps 11 bits, lo the next 11) plus 2^-25 in the scaled domain (lo's
 // subnormal spacing), i.e. 2^-39 of the slice maximum: fp32-class for every
-// finite x, whatever its magnitude.
+// finite x, whatever its magnitude.  (A staging path may scale by up to 12
+// below the optimal exponent -- max |x| * 2^e in [2^2, 2^15) -- which moves
+// that floor to 2^-27 of the maximum and leaves the 2^-22 |x| term.)
 //
 // Non-finite entries: the maximum is taken over |x| with NaN ignored and is
 // clamped to FLT_MAX, so a row holding +-inf keeps its finite entries in

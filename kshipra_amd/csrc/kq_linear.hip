@@ -457,52 +457,83 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
         }
       }
     } else {
-      // Every entry is parked raw in its own two LDS slots (32 bytes, the
-      // size of its hi / lo pair) until the row's scale is known: first the
-      // pre-loaded ones (freeing their registers), then the rest, loaded four
-      // slots per lane at a time with their loads issued together so the
-      // latencies overlap.  These loads come after the weights, so their use
-      // waits for the first weight batch.  (K short of the units' columns:
-      // the pre-loads skipped the K-tail entries, which are staged here with
-      // zeros past K.)  Each lane later reads back only what it parked.
-#pragma unroll
-      for (int j = 0; j < PRE; j++) {
-        if (j < pre_n && ((pre_mask >> j) & 1)) {
-          const int e = sub + lpr * j;
-          const float raw8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
-                                 xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
-          skinny_park<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, raw8);
-        }
-      }
-      for (int j0 = 0; j0 < per_lane; j0 += 4) {
-        float raw8[4][8];
-        bool need[4];
-        int ee[4];
+      // Entries beyond the pre-loads (loaded after the weights, four per lane
+      // at a time so their latencies overlap; K-tail entries, which the
+      // pre-loads skip, come here with zeros past K) are converted as they
+      // arrive, with a provisional exponent of the row-slice: 6 below the
+      // exponent of the largest |x| among the pre-loads (among the first four
+      // loaded entries when the pre-loads hold no nonzero value: those were
+      // converted to exact zeros / NaN, whatever the exponent), so every later
+      // entry up to 2^6 times larger still converts without overflow.  Once
+      // all are in, the row's true exponent e_true decides: with e_true - ex
+      // in [0, 12] the halves are exact to 2^-22 |x| + 2^(-39 + 12) max|x|
+      // (fp32-class) and stay; otherwise (a later entry more than ~64x the
+      // estimate, or an all-zero estimate) the lanes of that row load and
+      // convert their entries again with e_true.
+      auto row_max = [&](float v) { return lpr == 64 ? wave_max_uniform(v) : group_max(v, lpr); };
+      float raw8[4][8];
+      bool need[4];
+      int ee[4];
+      auto load4 = [&](int j0) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const int j = j0 + r;
           ee[r] = sub + lpr * j;
-          need[r] = row_lane && ee[r] < E && !(j < pre_n && ((pre_mask >> j) & 1));
+          need[r] = row_lane && j < per_lane && ee[r] < E && !(j < pre_n && ((pre_mask >> j) & 1));
           // row M: stage_load returns zeros without reading
           stage_load<BITS>(x, ldx, M, K, tb + (ee[r] >> 2), ee[r] & 3, need[r] ? my_m : M, xvec, raw8[r]);
         }
+      };
+      auto store4 = [&](int e_) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           if (need[r]) {
-            amax = absmax8(raw8[r], amax);
-            skinny_park<HL>(la, M, pitch, tb + (ee[r] >> 2), ee[r] & 3, my_m, raw8[r]);
+            half8_t hi, lo;
+            stage_convert<BITS>(raw8[r], e_, hi, lo);
+            skinny_store<HL>(la, M, pitch, tb + (ee[r] >> 2), ee[r] & 3, my_m, hi, lo);
           }
         }
-      }
-      ex = row_exponent(amax);
-      for (int j = 0; j < per_lane; j++) {
-        const int e = sub + lpr * j;
-        if (row_lane && e < E) {
-          float raw8[8];
-          skinny_unpark<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, raw8);
+      };
+      const float pmax = row_max(amax);
+      int ex_p = act_exponent(pmax) - 6;
+#pragma unroll
+      for (int j = 0; j < PRE; j++) {
+        if (j < pre_n && ((pre_mask >> j) & 1)) {
+          const int e = sub + lpr * j;
+          const float p8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
+                               xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
           half8_t hi, lo;
-          stage_convert<BITS>(raw8, ex, hi, lo);
+          stage_convert<BITS>(p8, ex_p, hi, lo);
           skinny_store<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, hi, lo);
+        }
+      }
+      load4(0);
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if (need[r]) amax = absmax8(raw8[r], amax);
+      if (!(pmax > 0.0f)) ex_p = act_exponent(row_max(amax)) - 6;
+      store4(ex_p);
+      for (int j0 = 4; j0 < per_lane; j0 += 4) {
+        load4(j0);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (need[r]) amax = absmax8(raw8[r], amax);
+        store4(ex_p);
+      }
+      const float gmax = row_max(amax);
+      const int e_true = act_exponent(gmax);
+      const bool keep = !(gmax > 0.0f) || (e_true - ex_p >= 0 && e_true - ex_p <= 12);
+      ex = keep ? ex_p : e_true;
+      if (!keep) {
+        for (int j = 0; j < per_lane; j++) {
+          const int e = sub + lpr * j;
+          if (row_lane && e < E) {
+            float r8[8];
+            stage_load<BITS>(x, ldx, M, K, tb + (e >> 2), e & 3, my_m, xvec, r8);
+            half8_t hi, lo;
+            stage_convert<BITS>(r8, ex, hi, lo);
+            skinny_store<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, hi, lo);
+          }
         }
       }
     }
