@@ -210,18 +210,20 @@ def batch_steps(int8, int4, dev, steps, warmup, eager, ms):
     return out
 
 
-def prefill_tflops(dev, steps, warmup, eager):
-    """Config: INT4 G=128 prefill chunk through one Llama-3-8B MLP."""
+def prefill_tflops(dev, steps, warmup, eager, scheme="int4"):
+    """Config: INT4 G=128 (or INT8) prefill chunk through one Llama-3-8B MLP."""
     g = torch.Generator(device=dev).manual_seed(7)
-    mk = lambda n, k: Proj(quantize_int4_per_group(torch.randn(n, k, device=dev, generator=g) * 0.02, 128), n, k, "int4")
+    qf = (lambda w: quantize_int4_per_group(w, 128)) if scheme == "int4" else quantize_int8_per_channel
+    mk = lambda n, k: Proj(qf(torch.randn(n, k, device=dev, generator=g) * 0.02), n, k, scheme)
     gate, up, down = mk(14336, 4096), mk(14336, 4096), mk(4096, 14336)
     lib = _lib.load()
     x = torch.randn(512, 4096, device=dev)
     a = torch.randn(512, 14336, device=dev)
     yg, yu, yd = (torch.empty(512, 14336, device=dev), torch.empty(512, 14336, device=dev),
                   torch.empty(512, 4096, device=dev))
-    wsb = max(lib.kq_linear_workspace_bytes(4, 512, 14336, 4096, 128),
-              lib.kq_linear_workspace_bytes(4, 512, 4096, 14336, 128))
+    bits = 4 if scheme == "int4" else 8
+    wsb = max(lib.kq_linear_workspace_bytes(bits, 512, 14336, 4096, 128),
+              lib.kq_linear_workspace_bytes(bits, 512, 4096, 14336, 128))
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
 
     def run():
@@ -532,10 +534,11 @@ def main():
     t_all = time.time()
     if args.only != "all":
         if args.only == "prefill":
-            pf = prefill_tflops(dev, args.steps, args.warmup, args.eager)
-            print(json.dumps({"section": "int4_prefill_m512_mlp", "tflops": round(pf["tflops"], 1),
-                              "ms": round(pf["ms"], 4), "gflop": round(pf["gflop"], 1),
-                              "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}))
+            for scheme in ("int4", "int8"):
+                pf = prefill_tflops(dev, args.steps, args.warmup, args.eager, scheme)
+                print(json.dumps({"section": f"{scheme}_prefill_m512_mlp", "tflops": round(pf["tflops"], 1),
+                                  "ms": round(pf["ms"], 4), "gflop": round(pf["gflop"], 1),
+                                  "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}))
         elif args.only == "m1":
             # M = 1 per projection, INT4 and INT8 (counter runs)
             res = {}
@@ -620,6 +623,10 @@ def main():
         breakdown["int4_prefill_m512_mlp"] = {"tflops": round(pf["tflops"], 1), "ms": round(pf["ms"], 3),
                                               "gflop": round(pf["gflop"], 1),
                                               "frac_of_fp16_mfma_peak": round(pf["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}
+        pf8 = prefill_tflops(dev, max(args.steps // 2, 3), 1, args.eager, "int8")
+        breakdown["int8_prefill_m512_mlp"] = {"tflops": round(pf8["tflops"], 1), "ms": round(pf8["ms"], 3),
+                                              "gflop": round(pf8["gflop"], 1),
+                                              "frac_of_fp16_mfma_peak": round(pf8["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4)}
         breakdown["lm_head_128256x4096"] = lm_head(dev, args.steps, args.warmup, args.eager)
         breakdown["attention_llama3_8b_heads"] = attention(dev, max(args.steps // 2, 3), 1, args.eager)
         cpu = cpu_baseline(dev)
