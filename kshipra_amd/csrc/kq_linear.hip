@@ -69,13 +69,14 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, int64_t 
 }
 
 // Permute the 8 loaded activations into operand-slot order, scale them by
-// 2^e and split them.
+// 2^e and split them (guard: wave_has_inf of the converting lanes' maxima).
 template <int BITS>
-__device__ __forceinline__ void stage_convert(const float (&raw8)[8], int e, half8_t& hi, half8_t& lo) {
+__device__ __forceinline__ void stage_convert(const float (&raw8)[8], int e, half8_t& hi, half8_t& lo,
+                                              bool guard) {
   float v[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) v[s] = raw8[kstep_perm<BITS>(s)];
-  split_hi_lo(v, e, hi, lo);
+  split_hi_lo(v, e, hi, lo, guard);
 }
 
 // Skinny layout: the two 16-byte slots of entry (T, qd, m).  HL: one array,
@@ -175,12 +176,13 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict
       amax = absmax8(raw[j], amax);
     }
     const int e = act_exponent(block_max(amax, red));
+    const bool guard = wave_has_inf(amax);
 #pragma unroll
     for (int j = 0; j < kStageHold; j++) {
       const int64_t q = threadIdx.x + (int64_t)j * blockDim.x;
       if (q < E) {
         half8_t hi, lo;
-        stage_convert<BITS>(raw[j], e, hi, lo);
+        stage_convert<BITS>(raw[j], e, hi, lo, guard);
         store(q, hi, lo);
       }
     }
@@ -192,11 +194,12 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict
       amax = absmax8(raw, amax);
     }
     const int e = act_exponent(block_max(amax, red));
+    const bool guard = wave_has_inf(amax);
     for (int64_t q = threadIdx.x; q < E; q += blockDim.x) {
       float raw[8];
       stage_load<BITS>(x, ldx, M, K, (int)(q >> 2), (int)(q & 3), m, xvec, raw);
       half8_t hi, lo;
-      stage_convert<BITS>(raw, e, hi, lo);
+      stage_convert<BITS>(raw, e, hi, lo, guard);
       store(q, hi, lo);
     }
     if (threadIdx.x == 0) rexp[m] = e;
@@ -444,6 +447,7 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
       // without a valid pre-load writes its (unused) values to the pad
       // column T = nT of row 0, which no lane reads.
       ex = row_exponent(amax);
+      const bool guard = wave_has_inf(amax);
 #pragma unroll
       for (int j = 0; j < PRE; j++) {
         if (M1 || j < pre_n) {
@@ -452,7 +456,7 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
           const float raw8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
                                  xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
           half8_t hi, lo;
-          stage_convert<BITS>(raw8, ex, hi, lo);
+          stage_convert<BITS>(raw8, ex, hi, lo, guard);
           skinny_store<HL>(la, M, pitch, ok ? tb + (e >> 2) : nT, e & 3, ok ? my_m : 0, hi, lo);
         }
       }
@@ -485,17 +489,19 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
         }
       };
       auto store4 = [&](int e_) {
+        const bool guard = wave_has_inf(amax);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           if (need[r]) {
             half8_t hi, lo;
-            stage_convert<BITS>(raw8[r], e_, hi, lo);
+            stage_convert<BITS>(raw8[r], e_, hi, lo, guard);
             skinny_store<HL>(la, M, pitch, tb + (ee[r] >> 2), ee[r] & 3, my_m, hi, lo);
           }
         }
       };
       const float pmax = row_max(amax);
       int ex_p = act_exponent(pmax) - 6;
+      const bool pguard = wave_has_inf(amax);
 #pragma unroll
       for (int j = 0; j < PRE; j++) {
         if (j < pre_n && ((pre_mask >> j) & 1)) {
@@ -503,7 +509,7 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
           const float p8[8] = {xa4[j][0], xa4[j][1], xa4[j][2], xa4[j][3],
                                xb4[j][0], xb4[j][1], xb4[j][2], xb4[j][3]};
           half8_t hi, lo;
-          stage_convert<BITS>(p8, ex_p, hi, lo);
+          stage_convert<BITS>(p8, ex_p, hi, lo, pguard);
           skinny_store<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, hi, lo);
         }
       }
@@ -525,13 +531,14 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
       const bool keep = !(gmax > 0.0f) || (e_true - ex_p >= 0 && e_true - ex_p <= 12);
       ex = keep ? ex_p : e_true;
       if (!keep) {
+        const bool guard = wave_has_inf(amax);
         for (int j = 0; j < per_lane; j++) {
           const int e = sub + lpr * j;
           if (row_lane && e < E) {
             float r8[8];
             stage_load<BITS>(x, ldx, M, K, tb + (e >> 2), e & 3, my_m, xvec, r8);
             half8_t hi, lo;
-            stage_convert<BITS>(r8, ex, hi, lo);
+            stage_convert<BITS>(r8, ex, hi, lo, guard);
             skinny_store<HL>(la, M, pitch, tb + (e >> 2), e & 3, my_m, hi, lo);
           }
         }
