@@ -141,16 +141,28 @@ __device__ __forceinline__ int wave_or(int v) {
 // add / fma removes the bias.  Output halves, in order:
 //   [q0, q4, q1, q5, q2, q6, q3, q7]  (slot s <-> nibble kPermInt4[s])
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ half8_t int4x8_to_half8(uint32_t w) {
+// The three constants a VOP3 instruction cannot take beside its one scalar
+// operand (the nibble masks and -72): a loop can hold them in VGPRs
+// (int4_consts_pinned) instead of rebuilding them for every word.
+struct Int4Consts {
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, b1 = 0xD480D480u;   // b1: (-72, -72) in fp16
+};
+__device__ __forceinline__ Int4Consts int4_consts_pinned() {
+  Int4Consts k;
+  __asm__ volatile("" : "+v"(k.mlo), "+v"(k.mhi), "+v"(k.b1));
+  return k;
+}
+
+__device__ __forceinline__ half8_t int4x8_to_half8(uint32_t w, const Int4Consts& k = Int4Consts{}) {
   // ((w ^ 0x88888888) & M) | 0x6400_6400 == (w & M) ^ (0x6400_6400 | (0x88888888 & M))
   const uint32_t w8 = w >> 8;
-  const half2_t t0 = __builtin_bit_cast(half2_t, (w & 0x000F000Fu) ^ 0x64086408u);
-  const half2_t t1 = __builtin_bit_cast(half2_t, (w & 0x00F000F0u) ^ 0x64806480u);
-  const half2_t t2 = __builtin_bit_cast(half2_t, (w8 & 0x000F000Fu) ^ 0x64086408u);
-  const half2_t t3 = __builtin_bit_cast(half2_t, (w8 & 0x00F000F0u) ^ 0x64806480u);
+  const half2_t t0 = __builtin_bit_cast(half2_t, (w & k.mlo) ^ 0x64086408u);
+  const half2_t t1 = __builtin_bit_cast(half2_t, (w & k.mhi) ^ 0x64806480u);
+  const half2_t t2 = __builtin_bit_cast(half2_t, (w8 & k.mlo) ^ 0x64086408u);
+  const half2_t t3 = __builtin_bit_cast(half2_t, (w8 & k.mhi) ^ 0x64806480u);
   const half2_t b0 = {(_Float16)1032.0f, (_Float16)1032.0f};
   const half2_t m1 = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const half2_t b1 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const half2_t b1 = __builtin_bit_cast(half2_t, k.b1);
   const half2_t r0 = t0 - b0;
   const half2_t r1 = t1 * m1 + b1;
   const half2_t r2 = t2 - b0;

@@ -574,22 +574,25 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 #pragma unroll
   for (int i = 0; i < TPU; i++) { ah[i] = half8_t{}; al[i] = half8_t{}; }
 
-  for (int64_t u0 = ub; u0 < ue; u0 += KS) {
-    if (u0 != ub) {
+  // Unit counters in 32 bits: their bounds checks stay scalar compares.
+  const int ub32 = (int)ub, ue32 = (int)ue;
+  [[maybe_unused]] const Int4Consts k4 = int4_consts_pinned();
+  for (int u0 = ub32; u0 < ue32; u0 += KS) {
+    if (u0 != ub32) {
       if constexpr (BITS == 4) {
 #pragma unroll
         for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], u0, ue, sv[t]);
       }
 #pragma unroll
       for (int u = 0; u < KS; u++) {
-        const int64_t unit = u0 + u < ue ? u0 + u : ue - 1;
+        const int64_t unit = u0 + u < ue32 ? u0 + u : ue32 - 1;
 #pragma unroll
         for (int t = 0; t < NT; t++) raw[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + unit * 64);
       }
     }
 #pragma unroll
     for (int u = 0; u < KS; u++) {
-      if (u0 + u < ue) {
+      if (u0 + u < ue32) {
         const int64_t unit = u0 + u;
         if (a_lane) {
 #pragma unroll
@@ -605,12 +608,14 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
             floatx4 g = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-              const half8_t b = int4x8_to_half8(raw[u][t][i]);
+              const half8_t b = int4x8_to_half8(raw[u][t][i], k4);
               g = mfma16x16x32(ah[i], b, g);
               if constexpr (!HL) g = mfma16x16x32(al[i], b, g);
             }
+            // One row: only accumulator row 0 (x's hi in lane quad 0, its lo
+            // in quad 2) is nonzero.
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[t][i] = __builtin_fmaf(s, g[i], acc[t][i]);
+            for (int i = 0; i < (M1 ? 1 : 4); i++) acc[t][i] = __builtin_fmaf(s, g[i], acc[t][i]);
           } else {
 #pragma unroll
             for (int j = 0; j < 2; j++) {
