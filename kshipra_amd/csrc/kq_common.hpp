@@ -262,54 +262,37 @@ __device__ __forceinline__ int act_exponent(float amax) {
 }
 
 // Split 8 fp32 activations (already in slot order) scaled by 2^e into fp16
-// hi/lo halves: per pair, one packed conversion for hi, a mixed-precision fma
-// each for the exact remainder t - hi, one packed conversion for lo.  GUARD
-// is needed only where an entry may be +-inf: there inf - inf = NaN becomes
-// lo = 0.  (lo must be 0, not merely finite: a large finite lo-row sum scaled
-// back by 2^-e could itself overflow and meet hi's inf with the opposite
-// sign.)  Without it a finite or NaN entry splits the same way.
-template <bool GUARD>
-__device__ __forceinline__ void split_hi_lo_g(const float (&v)[8], int e, half8_t& hi, half8_t& lo) {
-  if constexpr (GUARD) {
-#pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const float t = __builtin_amdgcn_ldexpf(v[s], e);
-      const _Float16 h = (_Float16)t;
-      const float d = t - (float)h;
-      hi[s] = h;
-      lo[s] = (_Float16)(d == d ? d : 0.0f);
-    }
-  } else {
-    // Per pair: hi = both halves rounded in one packed conversion; lo =
-    // fp16(fma(hi, -1, t)), the exact remainder rounded once, written into
-    // the low / high half by the mixed-precision fma (op_sel picks hi's half).
-    u32x4 h4, l4;
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const float t0 = __builtin_amdgcn_ldexpf(v[2 * p], e);
-      const float t1 = __builtin_amdgcn_ldexpf(v[2 * p + 1], e);
-      uint32_t h2, l2;
-      __asm__("v_cvt_pk_f16_f32 %0, %2, %3\n\t"
-              "v_fma_mixlo_f16 %1, %0, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
-              "v_fma_mixhi_f16 %1, %0, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-              : "=&v"(h2), "=&v"(l2)
-              : "v"(t0), "v"(t1));
-      h4[p] = h2;
-      l4[p] = l2;
-    }
-    hi = __builtin_bit_cast(half8_t, h4);
-    lo = __builtin_bit_cast(half8_t, l4);
-  }
-}
-
-// guard: wave-uniform, true when any lane of the wave may split a +-inf entry
-// (its running max |x| is inf); the common path skips the per-element check.
+// hi/lo halves.  Per pair: hi = both halves rounded in one packed conversion;
+// lo = fp16(fma(hi, -1, t)), the exact remainder rounded once, written into
+// the low / high half by the mixed-precision fma (op_sel picks hi's half).
+// guard: wave-uniform, true when some lane of the wave may split a +-inf
+// entry (its running max |x| is inf).  Such an entry has hi = +-inf and
+// lo = inf - inf = NaN; the guarded fix-up makes that lo 0.  (lo must be 0,
+// not merely finite: a large finite lo-row sum scaled back by 2^-e could
+// itself overflow and meet hi's inf with the opposite sign.)  A finite t has
+// |t| < 2^15, so hi = +-inf marks exactly the infinite entries; NaN stays NaN.
 __device__ __forceinline__ void split_hi_lo(const float (&v)[8], int e, half8_t& hi, half8_t& lo,
                                             bool guard) {
+  u32x4 h4, l4;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const float t0 = __builtin_amdgcn_ldexpf(v[2 * p], e);
+    const float t1 = __builtin_amdgcn_ldexpf(v[2 * p + 1], e);
+    uint32_t h2, l2;
+    __asm__("v_cvt_pk_f16_f32 %0, %2, %3\n\t"
+            "v_fma_mixlo_f16 %1, %0, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mixhi_f16 %1, %0, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=&v"(h2), "=&v"(l2)
+            : "v"(t0), "v"(t1));
+    h4[p] = h2;
+    l4[p] = l2;
+  }
+  hi = __builtin_bit_cast(half8_t, h4);
+  lo = __builtin_bit_cast(half8_t, l4);
   if (guard) {
-    split_hi_lo_g<true>(v, e, hi, lo);
-  } else {
-    split_hi_lo_g<false>(v, e, hi, lo);
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+      if (__builtin_isinf((float)hi[s])) lo[s] = (_Float16)0.0f;
   }
 }
 
