@@ -574,25 +574,23 @@ __global__ __launch_bounds__((skinny_max_threads<KS, NT>())) void skinny_kernel(
 #pragma unroll
   for (int i = 0; i < TPU; i++) { ah[i] = half8_t{}; al[i] = half8_t{}; }
 
-  // Unit counters in 32 bits: their bounds checks stay scalar compares.
-  const int ub32 = (int)ub, ue32 = (int)ue;
   [[maybe_unused]] const Int4Consts k4 = int4_consts_pinned();
-  for (int u0 = ub32; u0 < ue32; u0 += KS) {
-    if (u0 != ub32) {
+  for (int64_t u0 = ub; u0 < ue; u0 += KS) {
+    if (u0 != ub) {
       if constexpr (BITS == 4) {
 #pragma unroll
         for (int t = 0; t < NT; t++) load_scales<KS, SVEC>(srow[t], u0, ue, sv[t]);
       }
 #pragma unroll
       for (int u = 0; u < KS; u++) {
-        const int64_t unit = u0 + u < ue32 ? u0 + u : ue32 - 1;
+        const int64_t unit = u0 + u < ue ? u0 + u : ue - 1;
 #pragma unroll
         for (int t = 0; t < NT; t++) raw[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + unit * 64);
       }
     }
 #pragma unroll
     for (int u = 0; u < KS; u++) {
-      if (u0 + u < ue32) {
+      if (u0 + u < ue) {
         const int64_t unit = u0 + u;
         if (a_lane) {
 #pragma unroll
