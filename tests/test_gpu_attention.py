@@ -13,7 +13,8 @@
   tests' configurations, GQA g = 1 / 4 / 7, D = 64 / 128, block sizes that
   are and are not multiples of 16, shuffled block tables, prefix-only decode
   over long contexts (the split-key path), long prefill chunks, strided q /
-  out views, and device block tables.
+  out views, device block tables, and 30 seeded random configurations
+  (decode-like contexts up to 8k keys, chunks up to 96 queries).
 """
 
 from __future__ import annotations
@@ -177,3 +178,31 @@ def test_errors_mirror_the_reference(gpu):
                        torch.zeros((4, 1, 64), device=gpu), [32])
     out = chunked_attention(torch.zeros((8, 0, 64), device=gpu), kp, kp, [0], 5, 0, 16)
     assert out.shape == (8, 0, 64)
+
+
+def _random_case(i: int):
+    rng = np.random.default_rng(4242 + i)
+    h, hkv = [(4, 4), (8, 2), (32, 8), (28, 4), (14, 2), (16, 16), (2, 1), (12, 3)][int(rng.integers(8))]
+    d = int(rng.choice([64, 128]))
+    b = int(rng.choice([5, 12, 16, 20, 32, 48, 64]))
+    if i % 2 == 0:                                   # decode-like: few queries, long context
+        c, p = int(rng.integers(1, 5)), int(rng.integers(1, 8000))
+    else:                                            # chunk after a prefix
+        c, p = int(rng.integers(5, 97)), int(rng.integers(0, 800))
+    return h, hkv, c, p, d, b, bool(rng.random() < 0.7)
+
+
+@pytest.mark.parametrize("i", range(30))
+def test_random_attention_shapes(gpu, i):
+    """Seeded random heads / GQA group / head dim / block size / chunk / prefix /
+    block-table order against the float64 oracle, at the same bars."""
+    h, hkv, c, p, d, b, shuffle = _random_case(i)
+    q, kp, vp, table = _case(h, hkv, c, p, d, b, seed=7000 + i, shuffle=shuffle)
+    ref = att.chunked_attention(q, kp, vp, table, p, c, b)
+    name = f"random {i}: h={h} hkv={hkv} c={c} p={p} d={d} b={b} shuffle={shuffle}"
+    print(f"[attention {name}] launching", flush=True)
+    out = chunked_attention(torch.from_numpy(q).to(gpu), torch.from_numpy(kp).to(gpu),
+                            torch.from_numpy(vp).to(gpu), table, p, c, b)
+    torch.cuda.synchronize()
+    assert out.shape == (h, c, d)
+    _check(name, out.cpu().numpy(), ref, float(np.abs(vp).max()))
