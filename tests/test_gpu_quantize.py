@@ -4,7 +4,9 @@ Bar: payload and scales byte-identical to the C restatement of
 engine/quantization.py:196-344 on the same seeded fp32 inputs, including
 every adversarial branch (ties, zero rows, fp16-scale underflow -> +-inf ->
 clamp, subnormal and overflowing scales), the configs' full shapes, fp16 /
-bf16 inputs and strided inputs.
+bf16 inputs, strided inputs, and 24 seeded random shapes and value mixes
+(scales 2^-30 .. 2^30, zero / constant / outlier / tie rows) at every group
+size.
 """
 
 from __future__ import annotations
@@ -34,6 +36,40 @@ def _check_int4(w_np: np.ndarray, qw, g: int) -> None:
     assert qw.in_features_padded == kp and qw.group_size == g
     assert np.array_equal(qw.scales.cpu().numpy().view(np.uint16), s_ref.view(np.uint16))
     assert np.array_equal(qw.payload.cpu().numpy(), p_ref)
+
+
+def _random_weight(i: int):
+    """Seeded shape and value mix: Gaussian rows at scales 2^-30 .. 2^30,
+    some rows with outliers, all-zero rows, rows of one repeated value and
+    rows that put values exactly on rounding ties of their own scale."""
+    rng = np.random.default_rng(31337 + i)
+    n = int(rng.integers(1, 700))
+    k = int(rng.integers(1, 3000)) if i % 3 else int(rng.choice([128, 896, 4096]))
+    w = (rng.standard_normal((n, k)) * float(2.0 ** rng.integers(-30, 31))).astype(np.float32)
+    for r in rng.choice(n, size=min(n, 4), replace=False):
+        kind = int(rng.integers(4))
+        if kind == 0:
+            w[r] = 0.0
+        elif kind == 1:
+            w[r] = np.float32(rng.standard_normal())
+        elif kind == 2:
+            w[r, rng.integers(k)] *= 1000.0
+        else:                                   # multiples of half a step of the row's int8 scale
+            amax = max(float(np.abs(w[r]).max()), 1e-30)
+            step = amax / 127.0
+            w[r] = (rng.integers(-254, 255, size=k) * 0.5 * step).astype(np.float32)
+    return w
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_shapes_bit_exact(gpu, i):
+    """Seeded random shapes and value mixes: INT8, and INT4 at a random
+    supported group size, byte-identical with the oracle."""
+    w = _random_weight(i)
+    wd = torch.from_numpy(w).to(gpu)
+    _check_int8(w, quantize_int8_per_channel(wd))
+    g = [2, 32, 64, 128, 256][i % 5]
+    _check_int4(w, quantize_int4_per_group(wd, g), g)
 
 
 @pytest.mark.parametrize("k", [1, 7, 64, 128, 200, 896, 1000])
