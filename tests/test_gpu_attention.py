@@ -157,6 +157,31 @@ def test_paged_kv_write_bit_exact(gpu):
     assert np.array_equal(pool.cpu().numpy(), pool_np)
 
 
+@pytest.mark.parametrize("i", range(12))
+def test_paged_kv_write_random_bit_exact(gpu, i):
+    """Seeded random pool shapes, layers and slot mappings -- negative slots
+    and repeated slots (the later token wins) included -- bit-exact with the
+    oracle's store loop."""
+    rng = np.random.default_rng(500 + i)
+    nb, layers, hkv = int(rng.integers(1, 9)), int(rng.integers(1, 4)), int(rng.choice([1, 2, 4, 8]))
+    b, d = int(rng.choice([5, 12, 16, 64])), int(rng.choice([64, 128]))
+    layer = int(rng.integers(layers))
+    cap = nb * b
+    L = int(rng.integers(1, 2 * cap + 1))
+    slots = [int(s) for s in rng.integers(-cap, cap, size=L)]
+    pool_np = rng.standard_normal((nb, layers, 2, hkv, b, d)).astype(np.float32)
+    pool = torch.from_numpy(pool_np).to(gpu)
+    kflat = rng.standard_normal((L, hkv * d)).astype(np.float32)
+    vflat = rng.standard_normal((L, hkv * d)).astype(np.float32)
+    k = torch.from_numpy(kflat).to(gpu).view(1, L, hkv, d).transpose(1, 2)
+    v = torch.from_numpy(vflat).to(gpu).view(1, L, hkv, d).transpose(1, 2)
+    paged_kv_write(pool, layer, k, v, slots)
+    att.kv_write(pool_np, layer, kflat.reshape(L, hkv, d).transpose(1, 0, 2),
+                 vflat.reshape(L, hkv, d).transpose(1, 0, 2), slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.cpu().numpy(), pool_np), (nb, layers, hkv, b, d, L)
+
+
 def test_errors_mirror_the_reference(gpu):
     q = torch.zeros((6, 2, 64), device=gpu)
     kp = torch.zeros((4, 4, 16, 64), device=gpu)
